@@ -1,0 +1,191 @@
+"""Benchmark of the REAX FMHA path on one MI355X.
+
+Headline (the JSON `value`): causal GQA prefill, BASELINE config 2 (B 1, S 4096, Hq 32, Hkv 8, D 128, bf16),
+through reax_fmha_qx with LSE output, in causal-adjusted TFLOP/s (FLOPs = 4*Hq*D*P, P = S(S+1)/2 admitted
+pairs). A "step" is one attention forward over the resident inputs. Also reported in the same line:
+  - "roofline": the forward kernel's average duration from HIP events on its stream, against 2516.6 TFLOP/s
+    dense bf16 MFMA; "traffic" from the committed rocprofv3 PMC summary when present;
+  - "decode": config 4 (split-KV decode + LSE combine) in HBM GB/s against 8 TB/s, L2/MALL flushed between runs;
+  - "cpu_baseline": the OpenMP fp32 build of the CPU reference on a bounded sample of config 2's rows.
+Only N = 1 GPU is supported: the path is single-GPU by design.
+"""
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "reax-engine-kernels_amd"))
+
+from reax_fmha import workloads as W  # noqa: E402
+
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "fmha_fwd_c2_pmc.txt")
+
+
+def flush_buffer(torch):
+    return torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device="cuda")
+
+
+def bench_prefill(torch, ops, steps, warmup):
+    cfg = W.CONFIGS[2]
+    q, k, v, qpos = W.make_prefill_inputs(cfg)
+    dev = torch.device("cuda:0")
+    qd, kd, vd = (W.bits_to_torch(x, dev) for x in (q, k, v))
+    qp = torch.from_numpy(qpos).to(dev)
+    o = torch.empty_like(qd)
+    lse = torch.empty((cfg.B, cfg.Hq, cfg.S), dtype=torch.float32, device=dev)
+    scale = float(np.float32(cfg.scale))
+    run = lambda: ops.attention(qd, kd, vd, qp, scale=scale, o=o, lse=lse)
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    # timed region: exactly `steps` forwards, synchronised on both sides
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    # per-launch kernel duration with HIP events on the launch stream (torch's current stream)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for a, b in evs:
+        a.record()
+        run()
+        b.record()
+    torch.cuda.synchronize()
+    kms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    return cfg, wall, kms
+
+
+def bench_decode(torch, ops, iters):
+    cfg = W.CONFIGS[4]
+    q, k, v, qpos = W.make_decode_inputs(cfg)
+    dev = torch.device("cuda:0")
+    qd, kd, vd = (W.bits_to_torch(x, dev) for x in (q, k, v))
+    qp = torch.from_numpy(qpos).to(dev)
+    o = torch.empty_like(qd)
+    lse = torch.empty((cfg.B, cfg.Hq, cfg.S), dtype=torch.float32, device=dev)
+    ws = torch.empty(ops.splitkv_workspace_bytes(cfg.B, cfg.Hkv, cfg.S * cfg.G, cfg.D, cfg.num_splits),
+                     dtype=torch.uint8, device=dev)
+    scale = float(np.float32(cfg.scale))
+    run = lambda: ops.attention_splitkv(qd, kd, vd, qp, scale=scale, num_splits=cfg.num_splits, ws=ws, o=o, lse=lse)
+    fl = flush_buffer(torch)
+    for _ in range(3):
+        run()
+    times = []
+    for _ in range(iters):
+        fl.fill_(1)  # evict K/V from L2 and MALL (> 256 MB write)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        run()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+    del fl
+    ms = float(np.median(times))
+    gbs = cfg.decode_bytes() / (ms * 1e-3) / 1e9
+    return cfg, ms, gbs
+
+
+def pmc_traffic():
+    """HBM bytes per launch of the forward kernel from the committed rocprofv3 PMC summary, if present."""
+    if not os.path.exists(PMC_SUMMARY):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(PMC_SUMMARY).read())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(target_s=10.0):
+    """OpenMP fp32 CPU reference on a sample of config 2's query tokens (all heads, causal key counts),
+    scaled to TFLOP/s with the sample's own admitted-pair FLOPs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+
+    cfg = W.CONFIGS[2]
+    q, k, v, qpos = W.make_prefill_inputs(cfg)
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    st = W.natural_strides(cfg.B, cfg.S, cfg.Hq, cfg.N, cfg.Hkv, cfg.D)
+    rng = np.random.default_rng(5)
+
+    def run(ntok):
+        toks = np.sort(rng.choice(cfg.S, size=ntok, replace=False))
+        qs = np.ascontiguousarray(q[:, toks])
+        qps = np.ascontiguousarray(qpos[:, toks])
+        sst = dict(st, qsB=ntok * cfg.Hq * cfg.D)
+        t0 = time.perf_counter()
+        pyoracle.attention(qs, k, v, G=cfg.G, B=1, H=cfg.Hkv, M=ntok * cfg.G, N=cfg.N, D=cfg.D,
+                           scale=float(np.float32(cfg.scale)), strides=sst, qpos=qps, qpBs=ntok, precision="f32",
+                           nthreads=cores)
+        dt = time.perf_counter() - t0
+        flops = 4 * cfg.Hq * cfg.D * int((toks + 1).sum())
+        return ntok, dt, flops
+
+    ntok, dt, flops = run(32)
+    if dt < target_s:
+        ntok = int(min(cfg.S, max(32, 32 * target_s / max(dt, 1e-3))))
+        ntok, dt, flops = run(ntok)
+    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=cores, kind="port",
+                sample=f"config 2, {ntok} of {cfg.S} query tokens (seeded) x all {cfg.Hq} heads, causal keys; "
+                       f"{flops / 1e9:.1f} GFLOP in {dt:.1f} s, fp32 OpenMP CPU reference")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: the FMHA path runs on one GPU "
+              "(multi-GPU sharding is a design note only)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from reax_fmha import ops
+
+    cfg, wall, kms = bench_prefill(torch, ops, args.steps, args.warmup)
+    flops = cfg.flops()
+    value = flops / wall / 1e12
+    achieved = flops / (kms * 1e-3) / 1e12
+    traffic = pmc_traffic()
+    line = {
+        "metric": "causal attention TFLOP/s on 1 MI355X (% of bf16 MFMA peak); decode HBM GB/s",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: i.i.d. N(0,1) bf16 inputs from a fixed seed",
+        "config": {"workload": cfg.name, "B": cfg.B, "seq": cfg.S, "Hq": cfg.Hq, "Hkv": cfg.Hkv, "D": cfg.D,
+                   "causal": True, "flops_per_step": flops, "entry_point": "reax_fmha_qx (libreax_howu.so)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": W.BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / W.BF16_PEAK_TFLOPS, 4),
+                     "traffic": traffic, "kernel_ms": round(kms, 4)},
+    }
+    if not args.no_decode:
+        dcfg, dms, gbs = bench_decode(torch, ops, 20)
+        line["decode"] = {"workload": dcfg.name, "value": round(gbs, 1), "unit": "GB/s", "ms": round(dms, 4),
+                          "bytes": dcfg.decode_bytes(), "num_splits": dcfg.num_splits,
+                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
+                                       "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

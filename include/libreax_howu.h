@@ -1,0 +1,116 @@
+/* C ABI of libreax_howu.so, the MI355X (gfx950) rebuild of the reference's howu library.
+ *
+ * Conventions (as in the reference, libreax_howu/reax_fmha_v8.cu:434-450): caller-owned device pointers, the
+ * library allocates nothing (the split-KV entry takes a caller workspace), strides in elements, head-dim
+ * stride 1, asynchronous on `stream` (hipStream_t, NULL = default stream), return 0 or a hipError_t code.
+ * H is the KV-head count; folded row r of KV head h is query head h*G + r%G at token r/G.
+ *
+ * Three groups of symbols:
+ *   1. the reference's FMHA entry points (drop-in, head_dim 256);
+ *   2. extension entry points for what the reference ABI cannot express (head_dim 128, LSE output, two-stride
+ *      [S][Hq][D] row addressing, packed varlen sequences, split-KV decode with an LSE combine);
+ *   3. the reference's Gated-DeltaNet / norm / conv entry points, exported so that a loader which resolves every
+ *      symbol still loads this library. They are not implemented here: each returns REAX_ERR_NOT_IMPLEMENTED
+ *      (the *_smem queries return 0) and launches nothing.
+ */
+#ifndef LIBREAX_HOWU_H
+#define LIBREAX_HOWU_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipErrorNotSupported: returned by the entry points whose kernels are not part of this library. */
+#define REAX_ERR_NOT_IMPLEMENTED 801
+
+/* ---- 1. reference FMHA entry points ------------------------------------------------------------------- */
+
+/* Additive-bias attention. Replaces reax_fmha_b, libreax_howu/reax_fmha_v8.cu:434-442. */
+int reax_fmha_b(const void* q, const void* k, const void* v, const void* bias, void* o, float scale, int B, int H,
+                int M, int N, long long qsB, long long qsH, long long qsM, long long ksB, long long ksH, long long ksM,
+                long long vsB, long long vsH, long long vsM, long long bsB, long long bsH, long long bsM,
+                long long osB, long long osH, long long osM, void* stream);
+
+/* qpos / causal GQA attention. Replaces reax_fmha_q, libreax_howu/reax_fmha_v8.cu:443-450. */
+int reax_fmha_q(const void* q, const void* k, const void* v, const int* qpos, int G, long long qpBs, void* o,
+                float scale, int B, int H, int M, int N, long long qsB, long long qsH, long long qsM, long long ksB,
+                long long ksH, long long ksM, long long vsB, long long vsH, long long vsM, long long osB, long long osH,
+                long long osM, void* stream);
+
+/* ---- 2. extension entry points (no counterpart in the reference) --------------------------------------- */
+
+/* reax_fmha_q generalised (extends libreax_howu/reax_fmha_v8.cu:443-450):
+ *   - D in {128, 256};
+ *   - row r of (b, h) is read at q + b*qsB + h*qsH + (r/G)*qsT + (r%G)*qsG (reax_fmha_q is qsT = G*qsM,
+ *     qsG = qsM); for [B][S][Hq][D] tensors: qsB = S*Hq*D, qsH = G*D, qsT = Hq*D, qsG = D; O likewise;
+ *   - lse (optional, fp32): natural-log logsumexp of the scaled logits of each row, -inf for a row that sees
+ *     no key, written at lse + b*lsB + h*lsH + (r/G)*lsT + (r%G)*lsG. */
+int reax_fmha_qx(const void* q, const void* k, const void* v, const int* qpos, int G, long long qpBs, void* o,
+                 float* lse, float scale, int B, int H, int M, int N, int D, long long qsB, long long qsH,
+                 long long qsT, long long qsG, long long ksB, long long ksH, long long ksM, long long vsB,
+                 long long vsH, long long vsM, long long osB, long long osH, long long osT, long long osG,
+                 long long lsB, long long lsH, long long lsT, long long lsG, void* stream);
+
+/* Packed variable-length causal attention. Sequence b occupies tokens cu_seqlens[b] .. cu_seqlens[b+1]-1 of
+ * Q/O [T][Hq][D] and K/V [T][Hkv][D] (token strides qsT/ksT/vsT/osT, head strides qsH/ksH/vsH/osH); token i of
+ * a sequence sees that sequence's tokens 0..i only. cu_seqlens (int32, nseq+1 entries, device memory) starts at
+ * 0 and is non-decreasing; max_seqlen >= every sequence length. lse (optional) is [T][Hq] with strides
+ * lsT/lsH. Hq must be a multiple of Hkv. */
+int reax_fmha_varlen(const void* q, const void* k, const void* v, const int* cu_seqlens, int nseq, int max_seqlen,
+                     void* o, float* lse, float scale, int Hq, int Hkv, int D, long long qsT, long long qsH,
+                     long long ksT, long long ksH, long long vsT, long long vsH, long long osT, long long osH,
+                     long long lsT, long long lsH, void* stream);
+
+/* Bytes of device workspace reax_fmha_splitkv needs (0 for unsupported arguments). */
+size_t reax_fmha_splitkv_workspace(int B, int H, int M, int D, int num_splits);
+
+/* Split-KV attention for short query blocks (decode): same arguments and result as reax_fmha_qx, computed as
+ * num_splits independent key ranges (partial O and LSE in `ws`) merged by an LSE-weighted combine kernel.
+ * ws: device memory, 256-byte aligned, at least reax_fmha_splitkv_workspace(...) bytes, owned by the caller;
+ * it is overwritten, and calls that share it must be ordered on one stream. */
+int reax_fmha_splitkv(const void* q, const void* k, const void* v, const int* qpos, int G, long long qpBs, void* o,
+                      float* lse, float scale, int B, int H, int M, int N, int D, int num_splits, void* ws,
+                      size_t ws_bytes, long long qsB, long long qsH, long long qsT, long long qsG, long long ksB,
+                      long long ksH, long long ksM, long long vsB, long long vsH, long long vsM, long long osB,
+                      long long osH, long long osT, long long osG, long long lsB, long long lsH, long long lsT,
+                      long long lsG, void* stream);
+
+/* ---- 3. reference symbols outside the FMHA path (not implemented: return REAX_ERR_NOT_IMPLEMENTED) ------ */
+
+/* libreax_howu/reax_howu.cu:363-366 */
+int howu3_dense(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g, void* o,
+                const void* cu, float scale, int N, int H, int HV, void* stream);
+/* libreax_howu/reax_howu.cu:367-370 */
+int howu3_skip(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g, void* o,
+               const void* cu, float scale, int N, int H, int HV, void* stream);
+/* libreax_howu/reax_howu.cu:371 (returns 0 here: no kernel, no shared memory) */
+int howu3_smem(void);
+/* libreax_howu/reax_howu.cu:373-376 */
+int reax_howu(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g, void* o,
+              const void* cu, float scale, int N, int H, int HV, void* stream);
+/* libreax_howu/reax_kkt.cu:263-271 */
+int reax_kkt(const void* k, const void* g, const void* beta, void* A, const void* cu, const void* cidx, int NT, int H,
+             int HV, void* stream);
+/* libreax_howu/reax_kkt.cu:272 (returns 0 here) */
+int reax_kkt_smem(void);
+/* libreax_howu/reax_rarn_final.cu:98-106 */
+int reax_rarn(const void* part, int S, int serial, long long pstride, const void* res, const void* w, void* h_out,
+              void* out, int n, int D, float eps, float factor, void* stream);
+/* libreax_howu/reax_howu_norm_v3.cu:431-435 */
+int reax_howu_norm(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g,
+                   void* out, const void* cu, float scale, int N, int H, int HV, void* stream, const void* f2s,
+                   const void* z, long long ZS, const void* nw, float eps, float factor);
+/* libreax_howu/reax_conv_v2.cu:164-181 */
+int reax_conv_l2(const void* qkv, long long SX, const void* cache, int C, const void* meta, const void* w, void* q,
+                 void* k, void* v, int Tf, float eps, int KD, int VD, int rep, int skip_v, int RT, void* stream);
+/* libreax_howu/reax_conv_v2.cu:183-189 */
+int reax_conv_v(const void* qkv, long long SX, const void* cache, int C, const void* meta, const void* w, void* v,
+                int Tf, int KD, int VD, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,192 @@
+"""ctypes binding of the CPU oracle (liboracle_fmha.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke check in __graft_entry__.py and by the cpu_baseline
+leg of bench.py, always as the checker (or the timed CPU baseline), never as the product path.
+
+All array arguments are numpy arrays; bf16 tensors travel as uint16 bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle_fmha.so")
+
+MASK_QPOS, MASK_BIAS, MASK_VARLEN_CAUSAL, MASK_NONE = 0, 1, 2, 3
+
+MUTANTS = {
+    "no_scale": 1,
+    "gqa_head_major": 2,
+    "causal_strict": 3,
+    "no_normalise": 4,
+    "lse_log2": 5,
+    "sigmoid_sign": 6,
+    "gate_query_half": 7,
+    "combine_no_weight": 8,
+}
+
+
+class Args(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("qpos", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("cu_seqlens", ctypes.c_void_p),
+        ("qpBs", ctypes.c_int64),
+        ("bsB", ctypes.c_int64), ("bsH", ctypes.c_int64), ("bsM", ctypes.c_int64),
+        ("qsB", ctypes.c_int64), ("qsH", ctypes.c_int64), ("qsT", ctypes.c_int64), ("qsG", ctypes.c_int64),
+        ("ksB", ctypes.c_int64), ("ksH", ctypes.c_int64), ("ksM", ctypes.c_int64),
+        ("vsB", ctypes.c_int64), ("vsH", ctypes.c_int64), ("vsM", ctypes.c_int64),
+        ("mask_mode", ctypes.c_int32),
+        ("B", ctypes.c_int32), ("H", ctypes.c_int32), ("G", ctypes.c_int32),
+        ("M", ctypes.c_int32), ("N", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("key_lo", ctypes.c_int32), ("key_hi", ctypes.c_int32), ("p_bf16", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+    ]
+
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        L.oracle_attn_f64.restype = ctypes.c_int
+        L.oracle_attn_f64.argtypes = [ctypes.POINTER(Args), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_int32, ctypes.c_int32]
+        L.oracle_attn_f32.restype = ctypes.c_int
+        L.oracle_attn_f32.argtypes = L.oracle_attn_f64.argtypes
+        L.oracle_set_mutant.argtypes = [ctypes.c_int32]
+        L.oracle_get_mutant.restype = ctypes.c_int32
+        L.oracle_f64_to_bf16.restype = ctypes.c_uint16
+        L.oracle_f64_to_bf16.argtypes = [ctypes.c_double]
+        L.oracle_f64_to_bf16_array.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        L.oracle_sigmoid_bf16.restype = ctypes.c_uint16
+        L.oracle_sigmoid_bf16.argtypes = [ctypes.c_uint16]
+        L.oracle_sigmoid_bf16_all.argtypes = [ctypes.c_void_p]
+        L.oracle_post_gate.restype = ctypes.c_int
+        L.oracle_post_gate.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                       ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+                                       ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int64]
+        L.oracle_lse_combine.restype = ctypes.c_int
+        L.oracle_lse_combine.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                         ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+        L.oracle_args_size.restype = ctypes.c_int32
+        assert L.oracle_args_size() == ctypes.sizeof(Args), "oracle Args layout mismatch"
+        _lib = L
+    return _lib
+
+
+def set_mutant(name_or_id) -> None:
+    mid = MUTANTS[name_or_id] if isinstance(name_or_id, str) else int(name_or_id)
+    lib().oracle_set_mutant(mid)
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def _u16(a):
+    a = np.ascontiguousarray(a)
+    assert a.dtype == np.uint16, a.dtype
+    return a
+
+
+def attention(q, k, v, *, G, B, H, M, N, D, scale, strides, mask_mode=MASK_QPOS, qpos=None, qpBs=0,
+              bias=None, bias_strides=(0, 0, 0), cu_seqlens=None, key_lo=0, key_hi=0, p_bf16=False,
+              rows=None, precision="f64", nthreads=None):
+    """Runs the oracle on flat uint16 (bf16 bits) buffers q, k, v addressed through `strides`:
+    strides = dict(qsB, qsH, qsT, qsG, ksB, ksH, ksM, vsB, vsH, vsM), all in elements.
+
+    Returns (o, lse) as dense arrays o[B][H][M][D], lse[B][H][M] (float64 or float32). Entries of rows not
+    computed (outside `rows`, or beyond a varlen sequence) are NaN.
+    """
+    L = lib()
+    q, k, v = _u16(q), _u16(k), _u16(v)
+    keep = [q, k, v]
+    a = Args()
+    a.q, a.k, a.v = _ptr(q), _ptr(k), _ptr(v)
+    if qpos is not None:
+        qpos = np.ascontiguousarray(qpos, dtype=np.int32)
+        keep.append(qpos)
+        a.qpos = _ptr(qpos)
+    if bias is not None:
+        bias = _u16(bias)
+        keep.append(bias)
+        a.bias = _ptr(bias)
+    if cu_seqlens is not None:
+        cu_seqlens = np.ascontiguousarray(cu_seqlens, dtype=np.int32)
+        keep.append(cu_seqlens)
+        a.cu_seqlens = _ptr(cu_seqlens)
+    a.qpBs = qpBs
+    a.bsB, a.bsH, a.bsM = bias_strides
+    for name in ("qsB", "qsH", "qsT", "qsG", "ksB", "ksH", "ksM", "vsB", "vsH", "vsM"):
+        setattr(a, name, int(strides[name]))
+    a.mask_mode = mask_mode
+    a.B, a.H, a.G, a.M, a.N, a.D = B, H, G, M, N, D
+    a.key_lo, a.key_hi = key_lo, key_hi
+    a.p_bf16 = 1 if p_bf16 else 0
+    a.scale = scale
+    dt = np.float64 if precision == "f64" else np.float32
+    o = np.full((B, H, M, D), np.nan, dtype=dt)
+    lse = np.full((B, H, M), np.nan, dtype=dt)
+    rr = None
+    nr = 0
+    if rows is not None:
+        rr = np.ascontiguousarray(rows, dtype=np.int32)
+        nr = len(rr)
+        keep.append(rr)
+    nt = nthreads if nthreads else (os.cpu_count() or 1)
+    fn = L.oracle_attn_f64 if precision == "f64" else L.oracle_attn_f32
+    rc = fn(ctypes.byref(a), o.ctypes.data, lse.ctypes.data, _ptr(rr), nr, nt)
+    if rc != 0:
+        raise ValueError(f"oracle rejected arguments (rc={rc})")
+    return o, lse
+
+
+def f64_to_bf16(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float64)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f64_to_bf16_array(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def sigmoid_bf16_all() -> np.ndarray:
+    out = np.empty(65536, dtype=np.uint16)
+    lib().oracle_sigmoid_bf16_all(out.ctypes.data)
+    return out
+
+
+def post_gate(o, *, B, H, G, M, D, inv, Lq, qg, qg_rs, out, out_rs):
+    """Applies the POST epilogue to a dense oracle output o[B][H][M][D] in place into `out` (uint16)."""
+    o = np.ascontiguousarray(o, dtype=np.float64)
+    inv = np.ascontiguousarray(inv, dtype=np.int32)
+    qg = _u16(qg)
+    assert out.dtype == np.uint16 and out.flags.c_contiguous
+    rc = lib().oracle_post_gate(o.ctypes.data, B, H, G, M, D, inv.ctypes.data, Lq, qg.ctypes.data, qg_rs,
+                                out.ctypes.data, out_rs)
+    if rc != 0:
+        raise ValueError("oracle_post_gate rejected arguments")
+    return out
+
+
+def lse_combine(part_o, part_lse):
+    """part_o[S][R][D], part_lse[S][R] -> (o[R][D], lse[R])."""
+    part_o = np.ascontiguousarray(part_o, dtype=np.float64)
+    part_lse = np.ascontiguousarray(part_lse, dtype=np.float64)
+    S, R, D = part_o.shape
+    o = np.empty((R, D))
+    lse = np.empty(R)
+    rc = lib().oracle_lse_combine(part_o.ctypes.data, part_lse.ctypes.data, S, R, D, o.ctypes.data, lse.ctypes.data)
+    if rc != 0:
+        raise ValueError("oracle_lse_combine rejected arguments")
+    return o, lse

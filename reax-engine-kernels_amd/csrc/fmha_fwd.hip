@@ -1,0 +1,510 @@
+// FA2-style attention forward for gfx950 (CDNA4), the MI355X rebuild of the REAX FMHA path:
+//   reference: libreax_howu/reax_fmha_v8.cu (fmha3_kernel, launch2) and libreax_fmha_post/reax_fmha_v11.cu
+//   (the same kernel with the POST gate epilogue).
+//
+// Design (one workgroup = 4 wavefronts = 128 folded query rows of one (batch, KV head)):
+//   - A lane owns one query row: S^T = K . Q^T is computed with v_mfma_f32_32x32x16_bf16 where the A operand is
+//     a K fragment (32 keys x 16 dims, read from LDS) and the B operand is the lane's Q row fragment (kept in
+//     registers for the whole key loop). The 32x32 accumulator layout then gives lane l the scores of query
+//     l%32 for 16 keys, so the row max / row sum need only in-lane work plus one permlane32 swap.
+//   - The same registers, converted to bf16, are the B operand of O^T = V^T . P^T: no data movement between
+//     the two MFMA stages. The key order inside each 16-key MFMA step is permuted to match the accumulator
+//     layout, and V is stored transposed in LDS in that order so that every A operand is one 16-byte read.
+//   - K/V tiles of 64 keys are double-buffered in LDS (one barrier per tile). K rows use a 16-byte XOR swizzle
+//     (unit ^ (key & 15)); V^T rows use unit ^ ((dim & 7) ^ ((dim >> 3) & 7)): both the MFMA operand reads and
+//     the coalesced global->LDS copies are bank-conflict free.
+//   - Online softmax in base 2 on v_exp_f32 with the running max in log2 units; the O rescale is skipped when
+//     no row of the wavefront raised its max.
+//   - Causal / qpos tiles visit only key tiles that some row of the workgroup can see (v8:155-162, 237); the
+//     per-element mask is applied only to tiles that straddle a row's limit. Workgroups are dispatched heaviest
+//     first (v8:134-135) and, when B*H is a multiple of 8, each XCD's L2 serves a fixed set of KV heads.
+#include "fmha_common.h"
+#include "fmha_launch.h"
+
+#include <climits>
+
+namespace reax {
+
+template <int HD>
+struct FwdTile {
+  static constexpr int BM = 128;  // folded query rows per workgroup
+  static constexpr int BN = 64;   // keys per K/V tile
+  static constexpr int NT = 256;  // threads per workgroup
+  static constexpr int KU = HD / 8;  // 16-byte units per K row
+  static constexpr int UH = KU / 8;  // groups of 8 units per row
+  static constexpr int K_BYTES = BN * HD * 2;
+  static constexpr int V_BYTES = HD * BN * 2;
+  static constexpr int STAGE = K_BYTES + V_BYTES;
+  static constexpr int SMEM = 2 * STAGE;
+  static constexpr int K_LD = BN * KU / NT;        // 16-byte K loads per thread per tile
+  static constexpr int V_LD = (BN / 4) * KU / NT;  // (4 keys x 8 dims) V pieces per thread per tile
+  static constexpr int QK = HD / 16;               // MFMA k-steps of S^T = K Q^T
+  static constexpr int DB = HD / 32;               // 32-dim blocks of O^T
+  static_assert(HD == 128 || HD == 256, "head_dim 128 or 256");
+  static_assert(K_LD >= 1 && V_LD >= 1, "tile split");
+};
+
+// LDS byte offset of 16-byte unit u of key row j of the K tile.
+template <int HD>
+__device__ __forceinline__ uint32_t k_off(int j, int u) {
+  return (uint32_t)(j * (HD * 2) + ((u ^ (j & 15)) << 4));
+}
+// LDS byte offset of 16-byte unit U (8 keys in MFMA order) of dim row d of the V^T tile.
+template <int HD>
+__device__ __forceinline__ uint32_t vt_off(int d, int U) {
+  const int sw = (d & 7) ^ ((d >> 3) & 7);
+  return (uint32_t)(FwdTile<HD>::K_BYTES + d * (FwdTile<HD>::BN * 2) + ((U ^ sw) << 4));
+}
+
+template <int HD>
+struct Staging {
+  u32x4_t k[FwdTile<HD>::K_LD];
+  u32x4_t v[FwdTile<HD>::V_LD][4];
+};
+
+__device__ __forceinline__ u32x4_t ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+
+// Global -> registers for the K/V tile starting at key k0 (keys >= nkeys read as zero, so that masked
+// probabilities multiply finite values).
+template <int HD>
+__device__ __forceinline__ void load_tile(Staging<HD>& st, const uint16_t* Kb, const uint16_t* Vb, long long ksM,
+                                          long long vsM, int k0, int nkeys, int tid) {
+  using T = FwdTile<HD>;
+#pragma unroll
+  for (int i = 0; i < T::K_LD; ++i) {
+    const int idx = tid + T::NT * i, j = idx / T::KU, u = idx % T::KU, key = k0 + j;
+    st.k[i] = key < nkeys ? ld16(Kb + (long long)key * ksM + 8 * u) : u32x4_t{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int i = 0; i < T::V_LD; ++i) {
+    const int t = tid + T::NT * i;
+    const int e = (t >> 3) & 1, u = (t & 7) + 8 * ((t >> 4) % T::UH), U = t / (16 * T::UH);
+    const int kbase = k0 + 16 * (U >> 1) + 8 * e + 4 * (U & 1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = kbase + r;
+      st.v[i][r] = key < nkeys ? ld16(Vb + (long long)key * vsM + 8 * u) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+}
+
+// Registers -> LDS stage: K row-major (swizzled), V transposed into MFMA key order (swizzled).
+template <int HD>
+__device__ __forceinline__ void store_tile(const Staging<HD>& st, uint8_t* sb, int tid) {
+  using T = FwdTile<HD>;
+#pragma unroll
+  for (int i = 0; i < T::K_LD; ++i) {
+    const int idx = tid + T::NT * i, j = idx / T::KU, u = idx % T::KU;
+    *reinterpret_cast<u32x4_t*>(sb + k_off<HD>(j, u)) = st.k[i];
+  }
+#pragma unroll
+  for (int i = 0; i < T::V_LD; ++i) {
+    const int t = tid + T::NT * i;
+    const int e = (t >> 3) & 1, u = (t & 7) + 8 * ((t >> 4) % T::UH), U = t / (16 * T::UH);
+#pragma unroll
+    for (int dd = 0; dd < 8; ++dd) {
+      const int wd = dd >> 1;
+      const uint32_t x0 = st.v[i][0][wd], x1 = st.v[i][1][wd], x2 = st.v[i][2][wd], x3 = st.v[i][3][wd];
+      u32x2_t pr;
+      if (dd & 1) {
+        pr[0] = (x0 >> 16) | (x1 & 0xffff0000u);
+        pr[1] = (x2 >> 16) | (x3 & 0xffff0000u);
+      } else {
+        pr[0] = (x0 & 0xffffu) | (x1 << 16);
+        pr[1] = (x2 & 0xffffu) | (x3 << 16);
+      }
+      *reinterpret_cast<u32x2_t*>(sb + vt_off<HD>(8 * u + dd, U) + 8 * e) = pr;
+    }
+  }
+}
+
+__device__ __forceinline__ int wave_max(int x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x = max(x, __shfl_xor(x, off, 64));
+  return x;
+}
+__device__ __forceinline__ int wave_min(int x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x = min(x, __shfl_xor(x, off, 64));
+  return x;
+}
+
+template <int HD, int MODE, bool POST, bool SPLIT>
+__global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const FwdParams p, int o_vec8) {
+  using T = FwdTile<HD>;
+  __shared__ __align__(16) uint8_t smem[T::SMEM];
+  __shared__ int s_lim[4];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hf = lane >> 5, lr = lane & 31;
+
+  // ---- workgroup -> (batch, KV head, row tile[, key split]): heaviest tile first; when B*H % 8 == 0 each
+  // XCD (workgroups are dealt to the 8 XCDs round-robin) serves a fixed set of KV heads from its own L2
+  const int BH = p.B * p.H;
+  int id = blockIdx.x, split = 0;
+  if (SPLIT) {
+    split = id % p.num_splits;
+    id /= p.num_splits;
+  }
+  int bh, rank;
+  if (!SPLIT && (BH & 7) == 0) {
+    const int per = BH >> 3, x = id & 7, j = id >> 3;
+    bh = x + 8 * (j % per);
+    rank = j / per;
+  } else {
+    bh = id % BH;
+    rank = id / BH;
+  }
+  const int tile = p.n_tiles - 1 - rank;
+  const int b = bh / p.H, hk = bh - b * p.H;
+
+  long long tok0 = 0;
+  int Mb = p.M, Nb = p.N;
+  if (MODE == MODE_VARLEN) {
+    const int s0 = p.cu_seqlens[b], s1 = p.cu_seqlens[b + 1];
+    tok0 = s0;
+    Nb = s1 - s0;
+    Mb = Nb * p.G;
+  }
+  const int r0 = tile * T::BM;
+  if (r0 >= Mb) return;  // uniform over the workgroup (ragged varlen tail)
+
+  // ---- this lane's query row and its last visible key
+  const int r = r0 + 32 * w + lr;
+  const bool rvalid = r < Mb;
+  const int tok = rvalid ? r / p.G : 0;
+  const int g = rvalid ? r - tok * p.G : 0;
+  int lim = -1;
+  if (rvalid) {
+    if (MODE == MODE_QPOS) {
+      lim = min(p.qpos[(long long)b * p.qpBs + tok], Nb - 1);
+    } else if (MODE == MODE_VARLEN) {
+      lim = min(tok, Nb - 1);
+    } else {
+      lim = Nb - 1;
+    }
+    lim = max(lim, -1);
+  }
+  // key window of this workgroup: [kbeg, kend); split_len is a multiple of the tile size
+  int kbeg = 0, kend = Nb;
+  if (SPLIT) {
+    kbeg = split * p.split_len;
+    kend = min(Nb, kbeg + p.split_len);
+    lim = min(lim, kend - 1);
+    if (lim < kbeg) lim = -1;
+  }
+  const int wmax = wave_max(lim), wmin = wave_min(lim);
+  if (lane == 0) s_lim[w] = wmax;
+  __syncthreads();
+  const int cmax = max(max(s_lim[0], s_lim[1]), max(s_lim[2], s_lim[3]));
+  const int t_beg = kbeg / T::BN;
+  const int t_end = cmax < kbeg ? t_beg : cmax / T::BN + 1;  // key tiles [t_beg, t_end)
+
+  // ---- Q fragments: B operand of S^T = K Q^T (dims 16*ks + 8*hf .. +7 of this lane's row)
+  const uint16_t* qrow = p.q + (long long)b * p.qsB + (long long)hk * p.qsH + (tok0 + tok) * p.qsT + (long long)g * p.qsG;
+  bf16x8_t qf[T::QK];
+#pragma unroll
+  for (int ks = 0; ks < T::QK; ++ks)
+    qf[ks] = as_bf16x8(rvalid ? ld16(qrow + 16 * ks + 8 * hf) : u32x4_t{0u, 0u, 0u, 0u});
+
+  const uint16_t* Kb = p.k + (long long)b * p.ksB + (long long)hk * p.ksH + tok0 * p.ksM;
+  const uint16_t* Vb = p.v + (long long)b * p.vsB + (long long)hk * p.vsH + tok0 * p.vsM;
+
+  f32x16_t o[T::DB];
+#pragma unroll
+  for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  // BIAS mode turns the scores into log2-domain logits in place, so its exponent multiplier is 1
+  const float cc = MODE == MODE_BIAS ? 1.0f : p.scale_log2;
+  const uint16_t* brow = nullptr;
+  if (MODE == MODE_BIAS)
+    brow = p.bias + (long long)b * p.bsB + (long long)hk * p.bsH + (long long)(rvalid ? r : 0) * p.bsM;
+
+  Staging<HD> st;
+  if (t_end > t_beg) {
+    load_tile<HD>(st, Kb, Vb, p.ksM, p.vsM, t_beg * T::BN, kend, tid);
+    store_tile<HD>(st, smem, tid);
+  }
+  __syncthreads();
+
+  for (int t = t_beg; t < t_end; ++t) {
+    const int k0 = t * T::BN;
+    if (t + 1 < t_end) load_tile<HD>(st, Kb, Vb, p.ksM, p.vsM, k0 + T::BN, kend, tid);
+    const uint8_t* sb = smem + ((t - t_beg) & 1) * T::STAGE;
+    if (k0 <= wmax) {
+      // ---- S^T for 2 blocks of 32 keys: s[kb][v] is key k0 + 32kb + 8(v/4) + 4hf + v%4 of row lr
+      f32x16_t s[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < T::QK; ++ks) {
+          const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(sb + k_off<HD>(32 * kb + lr, 2 * ks + hf));
+          s[kb] = mfma32(as_bf16x8(kf), qf[ks], s[kb]);
+        }
+      }
+      if (MODE == MODE_BIAS) {
+        // x = (s*scale + bias) * log2(e), bias read only for keys inside the sequence (v8:279-280)
+        const float l2e = 1.44269504088896340736f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int key = k0 + 32 * kb + 8 * (v >> 2) + 4 * hf + (v & 3);
+            const float bv = (rvalid && key < Nb) ? __uint_as_float((uint32_t)brow[key] << 16) : 0.f;
+            s[kb][v] = (s[kb][v] * p.scale + bv) * l2e;
+          }
+      }
+      if (k0 + T::BN - 1 > wmin) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int key = k0 + 32 * kb + 8 * (v >> 2) + 4 * hf + (v & 3);
+            if (key > lim) s[kb][v] = -INFINITY;
+          }
+      }
+      // ---- online softmax (log2 domain)
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
+      mx = fmaxf(mx, swap_halves(mx));
+      const float m_new = fmaxf(m_run, mx * cc);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run - m_use);
+      float psum = 0.f;
+      uint32_t pk[2][8];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float p0 = fast_exp2(__builtin_fmaf(s[kb][2 * i], cc, -m_use));
+          const float p1 = fast_exp2(__builtin_fmaf(s[kb][2 * i + 1], cc, -m_use));
+          psum += p0;
+          psum += p1;
+          pk[kb][i] = pack_bf16x2(p0, p1);
+        }
+      l_run = l_run * alpha + psum;
+      if (__any(alpha != 1.0f)) {
+#pragma unroll
+        for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+      }
+      m_run = m_new;
+      // ---- O^T += V^T P^T, 4 MFMA k-steps of 16 keys
+#pragma unroll
+      for (int ss = 0; ss < 4; ++ss) {
+        const u32x4_t pw = {pk[ss >> 1][4 * (ss & 1) + 0], pk[ss >> 1][4 * (ss & 1) + 1], pk[ss >> 1][4 * (ss & 1) + 2],
+                            pk[ss >> 1][4 * (ss & 1) + 3]};
+        const bf16x8_t pb = as_bf16x8(pw);
+#pragma unroll
+        for (int db = 0; db < T::DB; ++db) {
+          const u32x4_t vf = *reinterpret_cast<const u32x4_t*>(sb + vt_off<HD>(32 * db + lr, 2 * ss + hf));
+          o[db] = mfma32(as_bf16x8(vf), pb, o[db]);
+        }
+      }
+    }
+    if (t + 1 < t_end) store_tile<HD>(st, smem + ((t + 1 - t_beg) & 1) * T::STAGE, tid);
+    __syncthreads();
+  }
+
+  // ---- epilogue: normalise, LSE, store (O^T layout: lane holds dims 32db + 8(v/4) + 4hf + v%4 of its row)
+  const float l = l_run + swap_halves(l_run);
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  if (!rvalid) return;
+  if (SPLIT) {
+    // partial result of this key split: O / l (fp32) and its LSE (natural log), -inf when nothing is visible
+    const long long prow = ((long long)bh * p.num_splits + split) * p.M + r;
+    if (hf == 0) p.ws_lse[prow] = l > 0.f ? (m_run + log2f(l)) * 0.69314718055994530942f : -INFINITY;
+    float* po = p.ws_o + prow * HD;
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = 32 * db + 8 * q4 + 4 * hf;
+        *reinterpret_cast<f32x4_t*>(po + d) =
+            f32x4_t{o[db][4 * q4 + 0] * inv, o[db][4 * q4 + 1] * inv, o[db][4 * q4 + 2] * inv, o[db][4 * q4 + 3] * inv};
+      }
+    return;
+  }
+  if (p.lse && hf == 0) {
+    const float lse = l > 0.f ? (m_run + log2f(l)) * 0.69314718055994530942f : -INFINITY;
+    p.lse[(long long)b * p.lsB + (long long)hk * p.lsH + (tok0 + tok) * p.lsT + (long long)g * p.lsG] = lse;
+  }
+  if (POST) {
+    // attn_post (v11:451-522): token row R = inv[b*Lq + tok], query head hk*G + g; R < 0 rows are padding
+    const int R = p.inv[(long long)b * p.Lq + tok];
+    if (R < 0) return;
+    const long long hq = (long long)hk * p.G + g;
+    const uint16_t* grow = p.qg + (long long)R * p.qg_rs + hq * (2 * HD) + HD;
+    uint16_t* orow = p.outp + (long long)R * p.out_rs + hq * HD;
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = 32 * db + 8 * q4 + 4 * hf;
+        const u32x2_t gw = *reinterpret_cast<const u32x2_t*>(grow + d);
+        const uint32_t ob0 = pack_bf16x2(o[db][4 * q4 + 0] * inv, o[db][4 * q4 + 1] * inv);
+        const uint32_t ob1 = pack_bf16x2(o[db][4 * q4 + 2] * inv, o[db][4 * q4 + 3] * inv);
+        const uint32_t s0 = sigmoid_bf16_bits(gw[0] & 0xffffu), s1 = sigmoid_bf16_bits(gw[0] >> 16);
+        const uint32_t s2 = sigmoid_bf16_bits(gw[1] & 0xffffu), s3 = sigmoid_bf16_bits(gw[1] >> 16);
+        u32x2_t res;
+        res[0] = pack_bf16x2(bf16lo(ob0) * bf16lo(s0), bf16hi(ob0) * bf16lo(s1));
+        res[1] = pack_bf16x2(bf16lo(ob1) * bf16lo(s2), bf16hi(ob1) * bf16lo(s3));
+        *reinterpret_cast<u32x2_t*>(orow + d) = res;
+      }
+    return;
+  }
+  if (!p.o) return;
+  uint16_t* orow = p.o + (long long)b * p.osB + (long long)hk * p.osH + (tok0 + tok) * p.osT + (long long)g * p.osG;
+#pragma unroll
+  for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = 32 * db + 8 * q4 + 4 * hf;
+      const uint32_t w0 = pack_bf16x2(o[db][4 * q4 + 0] * inv, o[db][4 * q4 + 1] * inv);
+      const uint32_t w1 = pack_bf16x2(o[db][4 * q4 + 2] * inv, o[db][4 * q4 + 3] * inv);
+      if (o_vec8) {
+        *reinterpret_cast<u32x2_t*>(orow + d) = u32x2_t{w0, w1};
+      } else {
+        *reinterpret_cast<uint32_t*>(orow + d) = w0;
+        *reinterpret_cast<uint32_t*>(orow + d + 2) = w1;
+      }
+    }
+}
+
+// LSE-weighted merge of the split partials: one wavefront per (b, kv head, row).
+//   lse = log(sum_s exp(lse_s)),  O = sum_s exp(lse_s - lse) * O_s     (O_s already normalised by its row sum)
+template <int HD>
+__global__ void __launch_bounds__(256) splitkv_combine_kernel(const FwdParams p) {
+  constexpr int DPL = HD / 64;  // dims per lane
+  const long long wid = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (wid >= (long long)p.B * p.H * p.M) return;
+  const int r = (int)(wid % p.M);
+  const long long bh = wid / p.M;
+  const int b = (int)(bh / p.H), hk = (int)(bh % p.H);
+  const int S = p.num_splits;
+  const long long base = bh * S * p.M + r;
+  float mx = -INFINITY;
+  for (int s = 0; s < S; ++s) mx = fmaxf(mx, p.ws_lse[base + (long long)s * p.M]);
+  float acc[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+  float wsum = 0.f;
+  if (mx != -INFINITY) {
+    for (int s = 0; s < S; ++s) {
+      const float wgt = fast_exp2((p.ws_lse[base + (long long)s * p.M] - mx) * 1.44269504088896340736f);
+      wsum += wgt;
+      if (wgt != 0.f) {
+        const float* po = p.ws_o + (base + (long long)s * p.M) * HD + DPL * lane;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[j] += wgt * po[j];
+      }
+    }
+  }
+  const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
+  const int tok = r / p.G, g = r - tok * p.G;
+  if (p.lse && lane == 0)
+    p.lse[(long long)b * p.lsB + (long long)hk * p.lsH + (long long)tok * p.lsT + (long long)g * p.lsG] =
+        wsum > 0.f ? mx + logf(wsum) : -INFINITY;
+  uint16_t* orow = p.o + (long long)b * p.osB + (long long)hk * p.osH + (long long)tok * p.osT + (long long)g * p.osG;
+#pragma unroll
+  for (int j = 0; j < DPL; j += 2)
+    *reinterpret_cast<uint32_t*>(orow + DPL * lane + j) = pack_bf16x2(acc[j] * inv, acc[j + 1] * inv);
+}
+
+// ------------------------------------------------------------------------------------------------ host side
+
+static bool aligned_elems(const void* ptr, long long n_elems_multiple, std::initializer_list<long long> strides) {
+  if ((reinterpret_cast<uintptr_t>(ptr) & (uintptr_t)(2 * n_elems_multiple - 1)) != 0) return false;
+  for (long long s : strides)
+    if (s % n_elems_multiple != 0) return false;
+  return true;
+}
+
+template <int HD, int MODE, bool POST, bool SPLIT>
+static int launch_fwd_t(const FwdParams& p, hipStream_t stream) {
+  using T = FwdTile<HD>;
+  const long long nwg = (long long)p.B * p.H * p.n_tiles * (SPLIT ? p.num_splits : 1);
+  if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  const int o_vec8 = (!POST && p.o) ? (aligned_elems(p.o, 4, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0) : 0;
+  hipLaunchKernelGGL((fmha_fwd_kernel<HD, MODE, POST, SPLIT>), dim3((unsigned)nwg), dim3(T::NT), 0, stream, p, o_vec8);
+  return (int)hipGetLastError();
+}
+
+// Argument checks shared by every forward entry point; fills the derived fields.
+static int prepare(FwdParams& p, bool post) {
+  // Input rows are read with 16-byte loads: bases and row strides must be multiples of 8 elements (the
+  // reference's cp.async has the same precondition, v8:169, 183, 191). O needs even strides (v8:396-397).
+  if (!p.q || !p.k || !p.v) return (int)hipErrorInvalidValue;
+  if (!aligned_elems(p.q, 8, {p.qsB, p.qsH, p.qsT, p.qsG}) || !aligned_elems(p.k, 8, {p.ksB, p.ksH, p.ksM}) ||
+      !aligned_elems(p.v, 8, {p.vsB, p.vsH, p.vsM}))
+    return (int)hipErrorInvalidValue;
+  if (p.o && !aligned_elems(p.o, 2, {p.osB, p.osH, p.osT, p.osG})) return (int)hipErrorInvalidValue;
+  if (post && (!p.inv || !p.qg || !p.outp || !aligned_elems(p.qg, 4, {p.qg_rs}) || !aligned_elems(p.outp, 4, {p.out_rs})))
+    return (int)hipErrorInvalidValue;
+  if (p.G <= 0 || p.B < 0 || p.H < 0 || p.M < 0 || p.N < 0) return (int)hipErrorInvalidValue;
+  p.scale_log2 = p.scale * 1.44269504088896340736f;
+  p.n_tiles = (int)(((long long)p.M + FwdTile<128>::BM - 1) / FwdTile<128>::BM);
+  return 0;
+}
+
+int launch_fwd(const FwdParams& p0, int head_dim, int mode, bool post, hipStream_t stream) {
+  FwdParams p = p0;
+  if (const int rc = prepare(p, post)) return rc;
+  if (head_dim == 128) {
+    if (mode == MODE_QPOS)
+      return post ? launch_fwd_t<128, MODE_QPOS, true, false>(p, stream) : launch_fwd_t<128, MODE_QPOS, false, false>(p, stream);
+    if (mode == MODE_BIAS && !post) return launch_fwd_t<128, MODE_BIAS, false, false>(p, stream);
+    if (mode == MODE_VARLEN && !post) return launch_fwd_t<128, MODE_VARLEN, false, false>(p, stream);
+  } else if (head_dim == 256) {
+    if (mode == MODE_QPOS)
+      return post ? launch_fwd_t<256, MODE_QPOS, true, false>(p, stream) : launch_fwd_t<256, MODE_QPOS, false, false>(p, stream);
+    if (mode == MODE_BIAS && !post) return launch_fwd_t<256, MODE_BIAS, false, false>(p, stream);
+    if (mode == MODE_VARLEN && !post) return launch_fwd_t<256, MODE_VARLEN, false, false>(p, stream);
+  }
+  return (int)hipErrorInvalidValue;
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t splitkv_workspace_bytes(int B, int H, int M, int head_dim, int num_splits) {
+  if (B <= 0 || H <= 0 || M <= 0 || num_splits <= 0 || (head_dim != 128 && head_dim != 256)) return 0;
+  const size_t rows = (size_t)B * H * num_splits * M;
+  return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
+}
+
+int launch_splitkv(const SplitParams& sp, int head_dim, hipStream_t stream) {
+  FwdParams p = sp.f;
+  if (const int rc = prepare(p, false)) return rc;
+  if (!p.o || sp.num_splits <= 0 || !sp.ws) return (int)hipErrorInvalidValue;
+  if (!aligned_elems(p.o, 2, {p.osB, p.osH, p.osT, p.osG})) return (int)hipErrorInvalidValue;
+  const size_t need = splitkv_workspace_bytes(p.B, p.H, p.M, head_dim, sp.num_splits);
+  if (need == 0 || sp.ws_bytes < need || (reinterpret_cast<uintptr_t>(sp.ws) & 255u)) return (int)hipErrorInvalidValue;
+  const size_t rows = (size_t)p.B * p.H * sp.num_splits * p.M;
+  p.ws_o = reinterpret_cast<float*>(sp.ws);
+  p.ws_lse = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(sp.ws) + align256(rows * head_dim * sizeof(float)));
+  p.num_splits = sp.num_splits;
+  const int per = (p.N + sp.num_splits - 1) / sp.num_splits;
+  p.split_len = ((per + FwdTile<128>::BN - 1) / FwdTile<128>::BN) * FwdTile<128>::BN;
+  if (p.split_len <= 0) p.split_len = FwdTile<128>::BN;
+  int rc = head_dim == 128 ? launch_fwd_t<128, MODE_QPOS, false, true>(p, stream)
+         : head_dim == 256 ? launch_fwd_t<256, MODE_QPOS, false, true>(p, stream)
+                           : (int)hipErrorInvalidValue;
+  if (rc) return rc;
+  const long long nrow = (long long)p.B * p.H * p.M;
+  const long long nwg = (nrow + 3) / 4;
+  if (nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  if (head_dim == 128)
+    hipLaunchKernelGGL(splitkv_combine_kernel<128>, dim3((unsigned)nwg), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(splitkv_combine_kernel<256>, dim3((unsigned)nwg), dim3(256), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
+}  // namespace reax

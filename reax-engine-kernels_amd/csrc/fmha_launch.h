@@ -1,0 +1,25 @@
+// Internal host-side launch interface shared by the C-ABI entry points.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "fmha_common.h"
+
+namespace reax {
+
+// Launches the forward kernel for head_dim 128 or 256 in one of the mask modes (MaskMode). Asynchronous on
+// `stream`; returns 0 or a hipError_t code (hipErrorInvalidValue for unsupported shapes or misaligned rows,
+// hipErrorInvalidConfiguration for an empty grid, as the reference's zero-sized launch would report).
+int launch_fwd(const FwdParams& p, int head_dim, int mode, bool post, hipStream_t stream);
+
+// Split-KV forward for short query blocks (decode): partial results per key split go to `ws`, then an LSE
+// combine kernel writes O (bf16) and the optional LSE. See fmha_splitkv.hip.
+struct SplitParams {
+  FwdParams f;     // q/k/v/o/lse, qpos, strides, B, H, G, M, N (rows per (b, kv head) = M)
+  int num_splits;  // key splits per (b, kv head)
+  void* ws;        // workspace (see splitkv_workspace_bytes)
+  size_t ws_bytes;
+};
+size_t splitkv_workspace_bytes(int B, int H, int M, int head_dim, int num_splits);
+int launch_splitkv(const SplitParams& p, int head_dim, hipStream_t stream);
+
+}  // namespace reax

@@ -1,0 +1,44 @@
+// Gated-DeltaNet / norm / conv entry points of libreax_howu.so that are outside the attention path.
+// They keep the reference prototypes (libreax_howu/reax_howu.cu:363-376, reax_kkt.cu:263-272,
+// reax_rarn_final.cu:98-106, reax_howu_norm_v3.cu:431-435, reax_conv_v2.cu:164-189) so that a loader which
+// resolves every symbol of the library still loads it, but launch nothing and return REAX_ERR_NOT_IMPLEMENTED.
+#pragma GCC visibility push(default)
+#include "libreax_howu.h"
+#pragma GCC visibility pop
+
+extern "C" {
+
+int howu3_dense(const void*, const void*, const void*, const void*, const void*, const void*, void*, const void*,
+                float, int, int, int, void*) {
+  return REAX_ERR_NOT_IMPLEMENTED;
+}
+int howu3_skip(const void*, const void*, const void*, const void*, const void*, const void*, void*, const void*, float,
+               int, int, int, void*) {
+  return REAX_ERR_NOT_IMPLEMENTED;
+}
+int howu3_smem(void) { return 0; }
+int reax_howu(const void*, const void*, const void*, const void*, const void*, const void*, void*, const void*, float,
+              int, int, int, void*) {
+  return REAX_ERR_NOT_IMPLEMENTED;
+}
+int reax_kkt(const void*, const void*, const void*, void*, const void*, const void*, int, int, int, void*) {
+  return REAX_ERR_NOT_IMPLEMENTED;
+}
+int reax_kkt_smem(void) { return 0; }
+int reax_rarn(const void*, int, int, long long, const void*, const void*, void*, void*, int, int, float, float,
+              void*) {
+  return REAX_ERR_NOT_IMPLEMENTED;
+}
+int reax_howu_norm(const void*, const void*, const void*, const void*, const void*, const void*, void*, const void*,
+                   float, int, int, int, void*, const void*, const void*, long long, const void*, float, float) {
+  return REAX_ERR_NOT_IMPLEMENTED;
+}
+int reax_conv_l2(const void*, long long, const void*, int, const void*, const void*, void*, void*, void*, int, float,
+                 int, int, int, int, int, void*) {
+  return REAX_ERR_NOT_IMPLEMENTED;
+}
+int reax_conv_v(const void*, long long, const void*, int, const void*, const void*, void*, int, int, int, void*) {
+  return REAX_ERR_NOT_IMPLEMENTED;
+}
+
+}  // extern "C"

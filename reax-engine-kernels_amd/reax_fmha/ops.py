@@ -1,0 +1,150 @@
+"""torch-facing wrappers over the C ABI (device tensors in, device tensors out, current HIP stream).
+
+Every call goes through libreax_howu.so / libreax_fmha_post.so; a nonzero return code raises. The tensors must
+live on the GPU: there is no CPU path.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import abi
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _check(name: str, rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{name} returned {rc}")
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("reax_fmha ops take device tensors only")
+
+
+# ---------------------------------------------------------------------------------------------- drop-in ABI
+
+def fmha_q(q, k, v, qpos, G, o, scale, *, lib="howu"):
+    """reax_fmha_q on folded tensors: q/o [B][H][M][256] (row r = token r/G, query head h*G + r%G),
+    k/v [B][N][H][256], qpos int32 [B][M/G]. Row strides are taken from the tensors."""
+    _dev(q, k, v, qpos, o)
+    B, H, M, D = q.shape
+    N = k.shape[1]
+    L = abi.howu() if lib == "howu" else abi.post()
+    rc = L.reax_fmha_q(q.data_ptr(), k.data_ptr(), v.data_ptr(), qpos.data_ptr(), G, qpos.stride(0), o.data_ptr(),
+                       scale, B, H, M, N, q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(2),
+                       k.stride(1), v.stride(0), v.stride(2), v.stride(1), o.stride(0), o.stride(1), o.stride(2),
+                       _stream())
+    _check("reax_fmha_q", rc)
+    return o
+
+
+def fmha_b(q, k, v, bias, o, scale, *, lib="howu"):
+    """reax_fmha_b: q/o [B][H][M][256], k/v [B][N][H][256], bias bf16 [B][H][M][N] (key stride 1)."""
+    _dev(q, k, v, bias, o)
+    B, H, M, D = q.shape
+    N = k.shape[1]
+    L = abi.howu() if lib == "howu" else abi.post()
+    rc = L.reax_fmha_b(q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(bias), o.data_ptr(), scale, B, H, M, N,
+                       q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(2), k.stride(1), v.stride(0),
+                       v.stride(2), v.stride(1),
+                       bias.stride(0) if bias is not None else 0, bias.stride(1) if bias is not None else 0,
+                       bias.stride(2) if bias is not None else 0,
+                       o.stride(0), o.stride(1), o.stride(2), _stream())
+    return rc
+
+
+def fmha_qp(q, k, v, qpos, G, scale, inv, Lq, qg, out):
+    """reax_fmha_qp (libreax_fmha_post.so): q [B][H][M][256] folded, k/v [B][N][H][256], inv int32 [B][Lq],
+    qg bf16 [T][Hq][512] (gate = second half), out bf16 [T][Hq*256]."""
+    _dev(q, k, v, qpos, inv, qg, out)
+    B, H, M, D = q.shape
+    N = k.shape[1]
+    rc = abi.post().reax_fmha_qp(q.data_ptr(), k.data_ptr(), v.data_ptr(), qpos.data_ptr(), G, qpos.stride(0),
+                                 scale, B, H, M, N, q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(2),
+                                 k.stride(1), v.stride(0), v.stride(2), v.stride(1), inv.data_ptr(), Lq,
+                                 qg.data_ptr(), qg.stride(0), out.data_ptr(), out.stride(0), _stream())
+    _check("reax_fmha_qp", rc)
+    return out
+
+
+# ---------------------------------------------------------------------------------------------- extensions
+
+def attention(q, k, v, qpos, *, scale, o=None, lse=None, want_lse=True):
+    """reax_fmha_qx on natural layouts: q [B][S][Hq][D], k/v [B][N][Hkv][D], qpos int32 [B][S]
+    (token m sees keys 0..qpos[b][m]). Returns (o [B][S][Hq][D] bf16, lse [B][Hq][S] fp32 or None)."""
+    _dev(q, k, v, qpos)
+    B, S, Hq, D = q.shape
+    N, Hkv = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    if o is None:
+        o = torch.empty_like(q)
+    if want_lse and lse is None:
+        lse = torch.empty((B, Hq, S), dtype=torch.float32, device=q.device)
+    ls = lse.stride() if lse is not None else (0, 0, 0)
+    rc = abi.howu().reax_fmha_qx(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), qpos.data_ptr(), G, qpos.stride(0), o.data_ptr(), _ptr(lse),
+        scale, B, Hkv, S * G, N, D,
+        q.stride(0), G * q.stride(2), q.stride(1), q.stride(2),
+        k.stride(0), k.stride(2), k.stride(1), v.stride(0), v.stride(2), v.stride(1),
+        o.stride(0), G * o.stride(2), o.stride(1), o.stride(2),
+        ls[0], G * ls[1], ls[2], ls[1], _stream())
+    _check("reax_fmha_qx", rc)
+    return o, lse
+
+
+def attention_varlen(q, k, v, cu_seqlens, max_seqlen, *, scale, o=None, lse=None, want_lse=True):
+    """reax_fmha_varlen: q/o [T][Hq][D], k/v [T][Hkv][D], cu_seqlens int32 [nseq+1] on the device.
+    Returns (o, lse [T][Hq] fp32 or None)."""
+    _dev(q, k, v, cu_seqlens)
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    nseq = cu_seqlens.numel() - 1
+    if o is None:
+        o = torch.empty_like(q)
+    if want_lse and lse is None:
+        lse = torch.empty((T, Hq), dtype=torch.float32, device=q.device)
+    ls = lse.stride() if lse is not None else (0, 0)
+    rc = abi.howu().reax_fmha_varlen(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens.data_ptr(), nseq, max_seqlen, o.data_ptr(), _ptr(lse),
+        scale, Hq, Hkv, D, q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+        o.stride(0), o.stride(1), ls[0], ls[1], _stream())
+    _check("reax_fmha_varlen", rc)
+    return o, lse
+
+
+def splitkv_workspace_bytes(B, Hkv, M, D, num_splits) -> int:
+    return abi.howu().reax_fmha_splitkv_workspace(B, Hkv, M, D, num_splits)
+
+
+def attention_splitkv(q, k, v, qpos, *, scale, num_splits, ws=None, o=None, lse=None, want_lse=True):
+    """reax_fmha_splitkv on natural layouts (as attention()); ws is a uint8 device tensor (allocated if None)."""
+    _dev(q, k, v, qpos)
+    B, S, Hq, D = q.shape
+    N, Hkv = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    M = S * G
+    need = splitkv_workspace_bytes(B, Hkv, M, D, num_splits)
+    if ws is None:
+        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    if o is None:
+        o = torch.empty_like(q)
+    if want_lse and lse is None:
+        lse = torch.empty((B, Hq, S), dtype=torch.float32, device=q.device)
+    ls = lse.stride() if lse is not None else (0, 0, 0)
+    rc = abi.howu().reax_fmha_splitkv(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), qpos.data_ptr(), G, qpos.stride(0), o.data_ptr(), _ptr(lse),
+        scale, B, Hkv, M, N, D, num_splits, ws.data_ptr(), ws.numel(),
+        q.stride(0), G * q.stride(2), q.stride(1), q.stride(2),
+        k.stride(0), k.stride(2), k.stride(1), v.stride(0), v.stride(2), v.stride(1),
+        o.stride(0), G * o.stride(2), o.stride(1), o.stride(2),
+        ls[0], G * ls[1], ls[2], ls[1], _stream())
+    _check("reax_fmha_splitkv", rc)
+    return o, lse

@@ -1,0 +1,75 @@
+"""CPU: the drop-in boundary. The two libraries load, export exactly the functions their headers declare (the
+reference's names plus the declared extensions), set no soname, and return the documented codes for calls that
+touch no GPU (NULL bias, not-implemented GDN entry points, workspace sizing)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from reax_fmha import abi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INC = os.path.join(ROOT, "include")
+
+
+def declared(header):
+    text = open(os.path.join(INC, header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(\w+)\s*\(", text, flags=re.M)))
+
+
+def exported_functions(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], check=True, capture_output=True, text=True).stdout
+    return sorted(line.split()[-1] for line in out.splitlines() if line.split()[1] == "T")
+
+
+@pytest.mark.parametrize("path,header,names", [
+    (abi.HOWU_PATH, "libreax_howu.h", abi.HOWU_SYMBOLS),
+    (abi.POST_PATH, "libreax_fmha_post.h", abi.POST_SYMBOLS),
+])
+def test_exports_match_header(path, header, names):
+    assert os.path.exists(path), f"{path} not built"
+    decl = declared(header)
+    assert decl == sorted(names), "header and binding disagree"
+    assert exported_functions(path) == decl
+
+
+def test_reference_names_present():
+    # reference: libreax_howu.so exports reax_fmha_b/q (v8:435, 444) and the GDN symbols; fmha_post its three
+    assert {"reax_fmha_b", "reax_fmha_q", "howu3_dense", "howu3_skip", "howu3_smem", "reax_howu", "reax_kkt",
+            "reax_kkt_smem", "reax_rarn", "reax_howu_norm", "reax_conv_l2", "reax_conv_v"} <= set(abi.HOWU_SYMBOLS)
+    assert abi.POST_SYMBOLS == ["reax_fmha_b", "reax_fmha_q", "reax_fmha_qp"]
+
+
+@pytest.mark.parametrize("path", [abi.HOWU_PATH, abi.POST_PATH])
+def test_no_soname(path):
+    out = subprocess.run(["readelf", "-d", path], check=True, capture_output=True, text=True).stdout
+    assert "SONAME" not in out
+
+
+@pytest.mark.parametrize("loader", [abi.howu, abi.post])
+def test_null_bias_returns_minus_one(loader):
+    L = loader()
+    args = [None] * 3 + [None, None, ctypes.c_float(0.1), 1, 1, 1, 1] + [0] * 15 + [None]
+    assert L.reax_fmha_b(*args) == -1  # v8:439: returns before any launch
+
+
+def test_gdn_entry_points_not_implemented():
+    L = abi.howu()
+    assert L.howu3_smem() == 0 and L.reax_kkt_smem() == 0
+    assert L.reax_howu(*([None] * 8 + [1.0, 1, 1, 1, None])) == abi.REAX_ERR_NOT_IMPLEMENTED
+    assert L.reax_kkt(*([None] * 6 + [1, 1, 2, None])) == abi.REAX_ERR_NOT_IMPLEMENTED
+    assert L.reax_rarn(None, 2, 0, 0, None, None, None, None, 1, 2560, 1e-6, 1.0, None) == abi.REAX_ERR_NOT_IMPLEMENTED
+    assert L.reax_conv_v(None, 0, None, 0, None, None, None, 1, 128, 128, None) == abi.REAX_ERR_NOT_IMPLEMENTED
+
+
+def test_splitkv_workspace_size():
+    L = abi.howu()
+    # config 4: B 16, Hkv 8, M = G = 4 rows, D 128, 16 splits: partial O fp32 + LSE fp32, each 256-byte aligned
+    rows = 16 * 8 * 16 * 4
+    want = -(-rows * 128 * 4 // 256) * 256 + -(-rows * 4 // 256) * 256
+    assert L.reax_fmha_splitkv_workspace(16, 8, 4, 128, 16) == want
+    assert L.reax_fmha_splitkv_workspace(16, 8, 4, 64, 16) == 0  # unsupported head_dim
+    assert L.reax_fmha_splitkv_workspace(16, 8, 4, 128, 0) == 0

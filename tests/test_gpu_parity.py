@@ -1,0 +1,364 @@
+"""GPU parity: the HIP kernels, called through the C ABI, against the double-precision CPU oracle (and the
+golden fixtures), to the tolerance of the path: bf16 outputs max-abs <= 2e-2 and mean-abs <= 2e-3, LSE within
+1e-3 relative (|dLSE| <= 1e-3 * max(1, |LSE|)). Large configurations are checked on a seeded subset of tokens
+(first and last tokens plus random ones; rows are independent) with every head."""
+import glob
+import os
+
+import numpy as np
+import pytest
+
+import fmha_cases as FC
+import pyoracle
+from reax_fmha import workloads as W
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+
+def _say(msg):
+    print(f"[gpu-parity] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from reax_fmha import abi
+
+    abi.howu()
+    abi.post()
+
+
+def dev(bits):
+    return W.bits_to_torch(bits, "cuda")
+
+
+def host(t):
+    return W.torch_to_bits(t)
+
+
+def run_qx(c: FC.Case, a: dict, want_lse=True):
+    from reax_fmha import ops
+
+    q, k, v = dev(a["q"]), dev(a["k"]), dev(a["v"])
+    qpos = torch.from_numpy(a["qpos"]).cuda()
+    o, lse = ops.attention(q, k, v, qpos, scale=c.scale, want_lse=want_lse)
+    torch.cuda.synchronize()
+    return host(o), (lse.cpu().numpy() if lse is not None else None)
+
+
+def token_subset(S, n_rand, seed, edge=64):
+    rng = np.random.default_rng(seed)
+    sel = set(range(min(edge, S))) | set(range(max(0, S - edge), S))
+    sel |= set(int(x) for x in rng.integers(0, S, size=n_rand))
+    return np.array(sorted(sel), dtype=np.int64)
+
+
+def oracle_on_tokens(c: FC.Case, a: dict, toks):
+    """Oracle rows for the given query tokens only (qpos keeps each token's own visibility)."""
+    sub = FC.Case(c.name + "_sub", B=c.B, S=len(toks), N=c.N, Hq=c.Hq, Hkv=c.Hkv, D=c.D, mode="qpos",
+                  qpos=a["qpos"][:, toks])
+    asub = dict(q=np.ascontiguousarray(a["q"][:, toks]), k=a["k"], v=a["v"], qpos=sub.qpos)
+    return FC.oracle_ref(sub, asub)
+
+
+# ------------------------------------------------------------------------------------------ qx (extension ABI)
+
+SMALL = [
+    FC.Case("c1_shape", B=1, S=512, N=512, Hq=8, Hkv=2, D=128, mode="causal", seed=1001),
+    FC.Case("ragged_s77_g4", B=2, S=77, N=77, Hq=8, Hkv=2, D=128, mode="causal", seed=3),
+    FC.Case("prefix_s50_n333", B=1, S=50, N=333, Hq=4, Hkv=4, D=128, mode="causal", seed=4),
+    FC.Case("g8_s200_d128", B=1, S=200, N=200, Hq=8, Hkv=1, D=128, mode="causal", seed=5),
+    FC.Case("full_s3_n1000", B=3, S=3, N=1000, Hq=8, Hkv=2, D=128, mode="full", seed=6),
+    FC.Case("d256_s300_g2", B=1, S=300, N=300, Hq=4, Hkv=2, D=256, mode="causal", seed=7),
+    FC.Case("d256_full_n129", B=2, S=17, N=129, Hq=2, Hkv=1, D=256, mode="full", seed=8),
+    FC.Case("n1_single_key", B=1, S=5, N=1, Hq=4, Hkv=2, D=128, mode="full", seed=9),
+]
+
+
+@pytest.mark.parametrize("c", SMALL, ids=lambda c: c.name)
+def test_qx_against_oracle(c):
+    _say(f"qx {c.name} B{c.B} S{c.S} N{c.N} Hq{c.Hq} Hkv{c.Hkv} D{c.D}")
+    a = FC.build(c)
+    og, lg = run_qx(c, a)
+    o, lse = FC.oracle_ref(c, a)
+    res = FC.check_tolerance(og, o, lg, lse, where=c.name)
+    _say(f"  {res}")
+
+
+def test_qx_qpos_edges():
+    """qpos < 0 rows give 0 / -inf; qpos = 0 rows reproduce V[0] exactly; qpos >= N sees every key."""
+    S, N = 40, 150
+    rng = np.random.default_rng(21)
+    qp = rng.integers(-2, N + 4, size=(1, S)).astype(np.int32)
+    qp[0, :4] = [0, -1, N + 3, 63]
+    c = FC.Case("qpos_edges", B=1, S=S, N=N, Hq=8, Hkv=2, D=128, mode="qpos", seed=22, qpos=qp)
+    _say("qx qpos_edges")
+    a = FC.build(c)
+    og, lg = run_qx(c, a)
+    o, lse = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, o, lg, lse, where=c.name)
+    dead = qp[0] < 0
+    assert (og[0, dead] == 0).all() and np.isneginf(lg[0][:, dead]).all()
+    zero = np.nonzero(qp[0] == 0)[0]
+    for m in zero:
+        for hq in range(c.Hq):
+            assert (og[0, m, hq] == a["v"][0, 0, hq // c.G]).all(), "qpos = 0 must write V[0] exactly"
+
+
+GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
+
+
+@pytest.mark.parametrize("path", GOLDEN, ids=lambda p: os.path.basename(p))
+def test_golden(path):
+    import golden_io
+
+    c, a, o_want, lse_want = golden_io.load(path)
+    _say(f"golden {c.name}")
+    if c.mode == "bias":
+        og = run_bias(c, a)
+        FC.check_tolerance(og, o_want, where=c.name)
+    else:
+        og, lg = run_qx(c, a)
+        FC.check_tolerance(og, o_want, lg, lse_want, where=c.name)
+
+
+# ------------------------------------------------------------------------------------------ drop-in ABI
+
+def fold(x, G):
+    """natural [B][S][Hq][D] -> folded [B][Hkv][S*G][D] (row r = m*G + g)."""
+    B, S, Hq, D = x.shape
+    return np.ascontiguousarray(x.reshape(B, S, Hq // G, G, D).transpose(0, 2, 1, 3, 4).reshape(B, Hq // G, S * G, D))
+
+
+def unfold(x, G):
+    B, H, M, D = x.shape
+    S = M // G
+    return x.reshape(B, H, S, G, D).transpose(0, 2, 1, 3, 4).reshape(B, S, H * G, D)
+
+
+@pytest.mark.parametrize("lib", ["howu", "post"])
+@pytest.mark.parametrize("S,G,Hkv", [(64, 8, 2), (45, 4, 1), (130, 1, 2)])
+def test_reax_fmha_q_dropin(lib, S, G, Hkv):
+    from reax_fmha import ops
+
+    c = FC.Case(f"q_{lib}_{S}_{G}", B=2, S=S, N=S, Hq=G * Hkv, Hkv=Hkv, D=256, mode="causal", seed=30 + S)
+    _say(f"reax_fmha_q {lib} S{S} G{G} Hkv{Hkv}")
+    a = FC.build(c)
+    q = dev(fold(a["q"], G))
+    k, v = dev(a["k"]), dev(a["v"])
+    qpos = torch.from_numpy(a["qpos"]).cuda()
+    o = torch.full_like(q, float("nan"))
+    ops.fmha_q(q, k, v, qpos, G, o, c.scale, lib=lib)
+    torch.cuda.synchronize()
+    og = unfold(host(o), G)
+    oref, _ = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, oref, where=c.name)
+
+
+def run_bias(c, a, lib="howu"):
+    from reax_fmha import ops
+
+    q = dev(fold(a["q"], 1))
+    k, v = dev(a["k"]), dev(a["v"])
+    bias = dev(a["bias"])
+    o = torch.full_like(q, float("nan"))
+    rc = ops.fmha_b(q, k, v, bias, o, c.scale, lib=lib)
+    assert rc == 0
+    torch.cuda.synchronize()
+    return unfold(host(o), 1)
+
+
+@pytest.mark.parametrize("lib", ["howu", "post"])
+def test_reax_fmha_b(lib):
+    c = FC.Case("bias", B=2, S=70, N=150, Hq=2, Hkv=2, D=256, mode="bias", seed=41, bias_neg_inf_frac=0.2,
+                bias_full_rows=(5, 69))
+    _say(f"reax_fmha_b {lib}")
+    a = FC.build(c)
+    og = run_bias(c, a, lib)
+    oref, _ = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, oref, where=c.name)
+    assert (og[:, [5, 69]] == 0).all(), "an all -inf bias row must give 0"
+
+
+def run_post(c, a, qg_bits, inv, T):
+    from reax_fmha import ops
+
+    G = c.G
+    q = dev(fold(a["q"], G))
+    k, v = dev(a["k"]), dev(a["v"])
+    qpos = torch.from_numpy(a["qpos"]).cuda()
+    qg = dev(qg_bits)
+    out = torch.from_numpy(np.full((T, c.Hq * c.D), 0x7E00, dtype=np.uint16).view(np.int16)).cuda().view(torch.bfloat16)
+    invd = torch.from_numpy(inv).cuda()
+    ops.fmha_qp(q, k, v, qpos, G, c.scale, invd, c.S, qg, out)
+    torch.cuda.synchronize()
+    return host(out)
+
+
+def test_reax_fmha_qp_post():
+    c = FC.Case("post", B=1, S=96, N=96, Hq=16, Hkv=2, D=256, mode="causal", seed=51)
+    _say("reax_fmha_qp post S96")
+    a = FC.build(c)
+    rng = np.random.default_rng(52)
+    T = c.S + 5
+    inv = rng.permutation(T)[: c.S].astype(np.int32)
+    inv[[3, 50]] = -1
+    qg = W.bf16_normal(rng, (T, c.Hq, 2 * c.D))
+    got = run_post(c, a, qg, inv, T)
+    o, _ = FC.oracle_ref(c, a)
+    want = np.full((T, c.Hq * c.D), 0x7E00, dtype=np.uint16)
+    pyoracle.post_gate(fold_dense(o, c.G), B=1, H=c.Hkv, G=c.G, M=c.S * c.G, D=c.D, inv=inv, Lq=c.S, qg=qg,
+                       qg_rs=c.Hq * 2 * c.D, out=want, out_rs=c.Hq * c.D)
+    untouched = np.setdiff1d(np.arange(T), inv[inv >= 0])
+    assert (got[untouched] == 0x7E00).all(), "rows not named by inv must stay untouched"
+    rows = inv[inv >= 0]
+    wf = W.bf16_bits_to_f32(want[rows]).astype(np.float64)
+    FC.check_tolerance(got[rows], wf, where="post")
+
+
+def fold_dense(o_nat, G):
+    B, S, Hq, D = o_nat.shape
+    return o_nat.reshape(B, S, Hq // G, G, D).transpose(0, 2, 1, 3, 4).reshape(B, Hq // G, S * G, D)
+
+
+def test_post_sigmoid_exhaustive():
+    """With V = 1 the attention output is exactly 1, so the POST output is the kernel's bf16 sigmoid of the gate:
+    every one of the 65,536 bf16 gate values must give the correctly rounded sigmoid (bit-exact)."""
+    S, G, Hkv, D = 16, 16, 1, 256
+    c = FC.Case("sig", B=1, S=S, N=S, Hq=G * Hkv, Hkv=Hkv, D=D, mode="causal", seed=61)
+    _say("post sigmoid exhaustive")
+    a = FC.build(c)
+    a["v"] = np.full_like(a["v"], 0x3F80)
+    gates = np.arange(65536, dtype=np.uint32).astype(np.uint16).reshape(S, G, D)
+    qg = np.zeros((S, G, 2 * D), dtype=np.uint16)
+    qg[:, :, D:] = gates
+    inv = np.arange(S, dtype=np.int32)
+    got = run_post(c, a, qg, inv, S).reshape(S, G, D)
+    want = pyoracle.sigmoid_bf16_all()[gates]
+    nan = np.isnan(W.bf16_bits_to_f32(want))
+    assert np.isnan(W.bf16_bits_to_f32(got[nan])).all()
+    bad = np.nonzero((got != want) & ~nan)
+    assert bad[0].size == 0, f"{bad[0].size} sigmoid mismatches, e.g. gate {gates[bad][:4]} -> {got[bad][:4]} vs {want[bad][:4]}"
+
+
+# ------------------------------------------------------------------------------------------ varlen
+
+def run_varlen(c, a, want_lse=True):
+    from reax_fmha import ops
+
+    q, k, v = dev(a["q"]), dev(a["k"]), dev(a["v"])
+    cu = torch.from_numpy(a["cu"]).cuda()
+    o, lse = ops.attention_varlen(q, k, v, cu, max(c.seqlens), scale=c.scale, want_lse=want_lse)
+    torch.cuda.synchronize()
+    return host(o), (lse.cpu().numpy() if lse is not None else None)
+
+
+@pytest.mark.parametrize("seqlens,D", [([5, 300, 0, 1, 129, 64], 128), ([200, 33, 97], 256)])
+def test_varlen_ragged(seqlens, D):
+    c = FC.Case("varlen", B=1, S=0, N=0, Hq=8, Hkv=2, D=D, mode="varlen", seed=71, seqlens=seqlens)
+    _say(f"varlen {seqlens} D{D}")
+    a = FC.build(c)
+    og, lg = run_varlen(c, a)
+    o, lse = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, o, lg, lse, where="varlen")
+
+
+def test_config3_varlen():
+    cfg = W.CONFIGS[3]
+    c = FC.Case(cfg.name, B=1, S=0, N=0, Hq=cfg.Hq, Hkv=cfg.Hkv, D=cfg.D, mode="varlen", seed=cfg.seed,
+                seqlens=cfg.seqlens)
+    _say(f"config 3 varlen {cfg.seqlens}")
+    q, k, v, cu = W.make_varlen_inputs(cfg)
+    a = dict(q=q, k=k, v=v, cu=cu)
+    og, lg = run_varlen(c, a)
+    o, lse = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, o, lg, lse, where="config3")
+
+
+# ------------------------------------------------------------------------------------------ split-KV decode
+
+def run_split(c, a, num_splits):
+    from reax_fmha import ops
+
+    q, k, v = dev(a["q"]), dev(a["k"]), dev(a["v"])
+    qpos = torch.from_numpy(a["qpos"]).cuda()
+    o, lse = ops.attention_splitkv(q, k, v, qpos, scale=c.scale, num_splits=num_splits)
+    torch.cuda.synchronize()
+    return host(o), lse.cpu().numpy()
+
+
+@pytest.mark.parametrize("num_splits", [1, 3, 16, 40])
+def test_splitkv_small(num_splits):
+    rng = np.random.default_rng(80)
+    B, N = 3, 1000
+    qp = np.array([[N - 1], [313], [-1]], dtype=np.int32)  # full cache, a shorter cache, an empty one
+    c = FC.Case("split", B=B, S=1, N=N, Hq=8, Hkv=2, D=128, mode="qpos", seed=81, qpos=qp)
+    _say(f"splitkv small S{num_splits}")
+    a = FC.build(c)
+    og, lg = run_split(c, a, num_splits)
+    o, lse = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, o, lg, lse, where=f"split{num_splits}")
+    assert (og[2] == 0).all() and np.isneginf(lg[2]).all()
+
+
+def test_splitkv_multitoken_d256():
+    c = FC.Case("split_mt", B=2, S=3, N=700, Hq=4, Hkv=2, D=256, mode="causal", seed=82)
+    _say("splitkv multi-token d256")
+    a = FC.build(c)
+    og, lg = run_split(c, a, 5)
+    o, lse = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, o, lg, lse, where="split_mt")
+
+
+def test_config4_decode():
+    cfg = W.CONFIGS[4]
+    _say("config 4 decode split-KV")
+    q, k, v, qpos = W.make_decode_inputs(cfg)
+    c = FC.Case(cfg.name, B=cfg.B, S=1, N=cfg.N, Hq=cfg.Hq, Hkv=cfg.Hkv, D=cfg.D, mode="qpos", qpos=qpos)
+    a = dict(q=q, k=k, v=v, qpos=qpos)
+    og, lg = run_split(c, a, cfg.num_splits)
+    o, lse = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, o, lg, lse, where="config4")
+
+
+# ------------------------------------------------------------------------------------------ full-size configs
+
+def test_config2_prefill():
+    cfg = W.CONFIGS[2]
+    _say("config 2 prefill S4096")
+    q, k, v, qpos = W.make_prefill_inputs(cfg)
+    c = FC.Case(cfg.name, B=1, S=cfg.S, N=cfg.N, Hq=cfg.Hq, Hkv=cfg.Hkv, D=cfg.D, mode="causal")
+    a = dict(q=q, k=k, v=v, qpos=qpos)
+    og, lg = run_qx(c, a)
+    toks = token_subset(cfg.S, 96, 7)
+    o, lse = oracle_on_tokens(c, a, toks)
+    FC.check_tolerance(og[:, toks], o, lg[:, :, toks], lse, where="config2")
+    # size-independent: every output finite, every LSE >= the LSE of key 0 alone (more keys never lower it)
+    assert np.isfinite(W.bf16_bits_to_f32(og)).all()
+
+
+def test_config5_post():
+    cfg = W.CONFIGS[5]
+    _say("config 5 long-context gated (reax_fmha_qp) S32768 D256")
+    q, k, v, qpos = W.make_prefill_inputs(cfg)
+    gate = W.make_gate(cfg)
+    c = FC.Case(cfg.name, B=1, S=cfg.S, N=cfg.N, Hq=cfg.Hq, Hkv=cfg.Hkv, D=cfg.D, mode="causal")
+    a = dict(q=q, k=k, v=v, qpos=qpos)
+    T = cfg.S
+    qg = np.empty((T, cfg.Hq, 2 * cfg.D), dtype=np.uint16)
+    qg[:, :, : cfg.D] = q[0]
+    qg[:, :, cfg.D:] = gate
+    del gate
+    inv = np.arange(T, dtype=np.int32)
+    got = run_post(c, a, qg, inv, T)
+    toks = token_subset(cfg.S, 24, 11, edge=16)
+    o, _ = oracle_on_tokens(c, a, toks)
+    sub_qg = np.ascontiguousarray(qg[toks])
+    want = np.zeros((len(toks), cfg.Hq * cfg.D), dtype=np.uint16)
+    pyoracle.post_gate(fold_dense(o, c.G), B=1, H=c.Hkv, G=c.G, M=len(toks) * c.G, D=c.D,
+                       inv=np.arange(len(toks), dtype=np.int32), Lq=len(toks), qg=sub_qg, qg_rs=cfg.Hq * 2 * cfg.D,
+                       out=want, out_rs=cfg.Hq * cfg.D)
+    FC.check_tolerance(got[toks], W.bf16_bits_to_f32(want).astype(np.float64), where="config5")
+    assert np.isfinite(W.bf16_bits_to_f32(got)).all()
