@@ -65,11 +65,19 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Exchange a value with the lane 32 positions away (the other half of the wavefront).
-__device__ __forceinline__ float swap_halves(float x) {
+// Combine a value with the one held 32 lanes away (the other half of the wavefront). v_permlane32_swap
+// exchanges the upper half of its first operand with the lower half of its second; with x in both, one result
+// holds the lower half's x in every lane and the other the upper half's, so max / sum of the two results give
+// the two-lane reduction in every lane.
+__device__ __forceinline__ float halves_max(float x) {
   const uint32_t u = __float_as_uint(x);
   const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return __uint_as_float(r[0]);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(u32x4_t x) { return __builtin_bit_cast(bf16x8_t, x); }

@@ -271,7 +271,7 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
-      mx = fmaxf(mx, swap_halves(mx));
+      mx = halves_max(mx);
       const float m_new = fmaxf(m_run, mx * cc);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
       const float alpha = fast_exp2(m_run - m_use);
@@ -313,7 +313,7 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
   }
 
   // ---- epilogue: normalise, LSE, store (O^T layout: lane holds dims 32db + 8(v/4) + 4hf + v%4 of its row)
-  const float l = l_run + swap_halves(l_run);
+  const float l = halves_sum(l_run);
   const float inv = l > 0.f ? 1.0f / l : 0.f;
   if (!rvalid) return;
   if (SPLIT) {

@@ -1,16 +1,7 @@
 """MI355X (gfx950) rebuild of the REAX engine's fused attention path.
 
 The product is the pair of C-ABI libraries in lib/ (libreax_howu.so, libreax_fmha_post.so). This package holds
-their ctypes binding (abi), torch-facing wrappers (ops) and the benchmark configurations (workloads).
+their ctypes binding (abi), torch-facing wrappers (ops, imported on demand: `from reax_fmha import ops`) and the
+benchmark configurations (workloads).
 """
 from . import abi, workloads  # noqa: F401
-
-__all__ = ["abi", "workloads", "ops"]
-
-
-def __getattr__(name):
-    if name == "ops":
-        from . import ops
-
-        return ops
-    raise AttributeError(name)
