@@ -143,7 +143,21 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "decode"], help="run one leg only (for profiling)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only run a 256 MiB device-to-device copy 5 times: the reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
+    if args.calib_copy:
+        import torch
+
+        src = torch.ones(256 * 1024 * 1024, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes_read": src.numel(), "calib_copy_bytes_written": dst.numel()}))
+        return
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: the FMHA path runs on one GPU "
               "(multi-GPU sharding is a design note only)", file=sys.stderr)
@@ -152,7 +166,14 @@ def main():
 
     from reax_fmha import ops
 
+    if args.only == "decode":
+        dcfg, dms, gbs = bench_decode(torch, ops, args.steps)
+        print(json.dumps({"decode_GBs": round(gbs, 1), "ms": round(dms, 4)}), flush=True)
+        return
     cfg, wall, kms = bench_prefill(torch, ops, args.steps, args.warmup)
+    if args.only == "prefill":
+        print(json.dumps({"TFLOPs": round(cfg.flops() / wall / 1e12, 2), "kernel_ms": round(kms, 4)}), flush=True)
+        return
     flops = cfg.flops()
     value = flops / wall / 1e12
     achieved = flops / (kms * 1e-3) / 1e12

@@ -27,95 +27,87 @@ namespace reax {
 
 template <int HD>
 struct FwdTile {
-  static constexpr int BM = 128;  // folded query rows per workgroup
-  static constexpr int BN = 64;   // keys per K/V tile
-  static constexpr int NT = 256;  // threads per workgroup
-  static constexpr int KU = HD / 8;  // 16-byte units per K row
-  static constexpr int UH = KU / 8;  // groups of 8 units per row
-  static constexpr int K_BYTES = BN * HD * 2;
-  static constexpr int V_BYTES = HD * BN * 2;
-  static constexpr int STAGE = K_BYTES + V_BYTES;
-  static constexpr int SMEM = 2 * STAGE;
-  static constexpr int K_LD = BN * KU / NT;        // 16-byte K loads per thread per tile
-  static constexpr int V_LD = (BN / 4) * KU / NT;  // (4 keys x 8 dims) V pieces per thread per tile
-  static constexpr int QK = HD / 16;               // MFMA k-steps of S^T = K Q^T
-  static constexpr int DB = HD / 32;               // 32-dim blocks of O^T
+  static constexpr int BM = 128;       // folded query rows per workgroup (4 wavefronts x 32)
+  static constexpr int BN = 64;        // keys per K/V tile
+  static constexpr int NT = 256;       // threads per workgroup
+  static constexpr int KU = HD / 8;    // 16-byte units per K/V row
+  static constexpr int TILE = BN * HD * 2;  // bytes of one K or V tile
+  static constexpr int DMA = TILE / 1024;   // 64-lane x 16-byte direct-to-LDS loads per tile
+  static constexpr int DMA_W = DMA / 4;     // ... per wavefront
+  static constexpr int QK = HD / 16;        // MFMA k-steps of S^T = K Q^T
+  static constexpr int DB = HD / 32;        // 32-dim blocks of O^T
   static_assert(HD == 128 || HD == 256, "head_dim 128 or 256");
-  static_assert(K_LD >= 1 && V_LD >= 1, "tile split");
 };
 
-// LDS byte offset of 16-byte unit u of key row j of the K tile.
+// Row-major K/V tiles with a 16-byte-unit XOR swizzle. For 8 consecutive rows f() takes 8 distinct values
+// (conflict-free 16-byte K operand reads of 8 rows at one unit), and for 4 consecutive rows f()/2 takes 4
+// distinct values (conflict-free transposed V reads: 4 rows x 2 adjacent units per 16-lane group).
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1) | (r & 8); }
 template <int HD>
-__device__ __forceinline__ uint32_t k_off(int j, int u) {
-  return (uint32_t)(j * (HD * 2) + ((u ^ (j & 15)) << 4));
+__device__ __forceinline__ uint32_t tile_off(int r, int u) {
+  return (uint32_t)(r * (HD * 2) + ((u ^ swz(r)) << 4));
 }
-// LDS byte offset of 16-byte unit U (8 keys in MFMA order) of dim row d of the V^T tile.
-template <int HD>
-__device__ __forceinline__ uint32_t vt_off(int d, int U) {
-  const int sw = (d & 7) ^ ((d >> 3) & 7);
-  return (uint32_t)(FwdTile<HD>::K_BYTES + d * (FwdTile<HD>::BN * 2) + ((U ^ sw) << 4));
-}
-
-template <int HD>
-struct Staging {
-  u32x4_t k[FwdTile<HD>::K_LD];
-  u32x4_t v[FwdTile<HD>::V_LD][4];
-};
 
 __device__ __forceinline__ u32x4_t ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
 
-// Global -> registers for the K/V tile starting at key k0 (keys >= nkeys read as zero, so that masked
-// probabilities multiply finite values).
+#define REAX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// Direct global -> LDS copy of the K or V tile at key k0 into `buf` (this wavefront's share). Lane l of load c
+// fills bytes [c*1024 + 16 l, +16) of the tile, i.e. row r, swizzled unit pu; it fetches the logical unit that
+// belongs there. Keys past the window are clamped to its last key: their scores are masked, so they only ever
+// meet a zero probability.
 template <int HD>
-__device__ __forceinline__ void load_tile(Staging<HD>& st, const uint16_t* Kb, const uint16_t* Vb, long long ksM,
-                                          long long vsM, int k0, int nkeys, int tid) {
+__device__ __forceinline__ void dma_tile(uint8_t* buf, const uint16_t* base, long long stride, int k0, int kend,
+                                         int w, int lane) {
   using T = FwdTile<HD>;
 #pragma unroll
-  for (int i = 0; i < T::K_LD; ++i) {
-    const int idx = tid + T::NT * i, j = idx / T::KU, u = idx % T::KU, key = k0 + j;
-    st.k[i] = key < nkeys ? ld16(Kb + (long long)key * ksM + 8 * u) : u32x4_t{0u, 0u, 0u, 0u};
+  for (int i = 0; i < T::DMA_W; ++i) {
+    const int c = w * T::DMA_W + i;
+    const int byte = c * 1024 + 16 * lane;
+    const int r = byte / (HD * 2), pu = (byte % (HD * 2)) >> 4;
+    const int u = pu ^ swz(r);
+    const int key = min(k0 + r, kend - 1);
+    __builtin_amdgcn_global_load_lds(base + (long long)key * stride + 8 * u, REAX_LDS(buf + c * 1024), 16, 0, 0);
   }
+}
+
+__device__ __forceinline__ void wait_dma_and_sync() {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's direct-to-LDS loads have landed
+  __syncthreads();                     // ... and every other wavefront's
+}
+
+// S^T for one 64-key tile: s[kb][v] = score of this lane's row against key 32kb + 8(v/4) + 4hf + v%4.
+template <int HD>
+__device__ __forceinline__ void qk_tile(f32x16_t (&s)[2], const uint8_t* kb_, const bf16x8_t (&qf)[HD / 16], int lr,
+                                        int hf) {
 #pragma unroll
-  for (int i = 0; i < T::V_LD; ++i) {
-    const int t = tid + T::NT * i;
-    const int e = (t >> 3) & 1, u = (t & 7) + 8 * ((t >> 4) % T::UH), U = t / (16 * T::UH);
-    const int kbase = k0 + 16 * (U >> 1) + 8 * e + 4 * (U & 1);
+  for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int key = kbase + r;
-      st.v[i][r] = key < nkeys ? ld16(Vb + (long long)key * vsM + 8 * u) : u32x4_t{0u, 0u, 0u, 0u};
+    for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) {
+      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb_ + tile_off<HD>(32 * kb + lr, 2 * ks + hf));
+      s[kb] = mfma32(as_bf16x8(kf), qf[ks], s[kb]);
     }
   }
 }
 
-// Registers -> LDS stage: K row-major (swizzled), V transposed into MFMA key order (swizzled).
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+// V^T operand (32 dims x 16 keys in MFMA key order) of dim block db, k-step ss, from the row-major V tile with
+// two ds_read_b64_tr_b16: in each 16-lane group, lane i reads 4 dims of key row (i/4) and receives 4 keys of
+// dim (i%16) back.
 template <int HD>
-__device__ __forceinline__ void store_tile(const Staging<HD>& st, uint8_t* sb, int tid) {
-  using T = FwdTile<HD>;
-#pragma unroll
-  for (int i = 0; i < T::K_LD; ++i) {
-    const int idx = tid + T::NT * i, j = idx / T::KU, u = idx % T::KU;
-    *reinterpret_cast<u32x4_t*>(sb + k_off<HD>(j, u)) = st.k[i];
-  }
-#pragma unroll
-  for (int i = 0; i < T::V_LD; ++i) {
-    const int t = tid + T::NT * i;
-    const int e = (t >> 3) & 1, u = (t & 7) + 8 * ((t >> 4) % T::UH), U = t / (16 * T::UH);
-#pragma unroll
-    for (int dd = 0; dd < 8; ++dd) {
-      const int wd = dd >> 1;
-      const uint32_t x0 = st.v[i][0][wd], x1 = st.v[i][1][wd], x2 = st.v[i][2][wd], x3 = st.v[i][3][wd];
-      u32x2_t pr;
-      if (dd & 1) {
-        pr[0] = (x0 >> 16) | (x1 & 0xffff0000u);
-        pr[1] = (x2 >> 16) | (x3 & 0xffff0000u);
-      } else {
-        pr[0] = (x0 & 0xffffu) | (x1 << 16);
-        pr[1] = (x2 & 0xffffu) | (x3 << 16);
-      }
-      *reinterpret_cast<u32x2_t*>(sb + vt_off<HD>(8 * u + dd, U) + 8 * e) = pr;
-    }
-  }
+__device__ __forceinline__ bf16x8_t v_operand(const uint8_t* vb, int db, int ss, int lane) {
+  const int h = lane >> 5, dh = (lane >> 4) & 1, i = lane & 15;
+  const int row = 16 * ss + 4 * h + (i >> 2);
+  const int u = 4 * db + 2 * dh + ((i & 3) >> 1);
+  const uint8_t* p0 = vb + tile_off<HD>(row, u) + 8 * (i & 1);
+  const uint8_t* p1 = vb + tile_off<HD>(row + 8, u) + 8 * (i & 1);
+  const i16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(p0));
+  const i16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(p1));
+  const u32x2_t ua = __builtin_bit_cast(u32x2_t, a), ub = __builtin_bit_cast(u32x2_t, b);
+  return as_bf16x8(u32x4_t{ua[0], ua[1], ub[0], ub[1]});
 }
 
 __device__ __forceinline__ int wave_max(int x) {
@@ -129,10 +121,17 @@ __device__ __forceinline__ int wave_min(int x) {
   return x;
 }
 
+// Lazy rescaling: the running max (log2 units) is raised only when a tile's max exceeds it by more than
+// RESCALE_SLACK, so probabilities stay below 2^RESCALE_SLACK and the O / row-sum rescale is rare.
+constexpr float RESCALE_SLACK = 8.0f;
+
 template <int HD, int MODE, bool POST, bool SPLIT>
 __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const FwdParams p, int o_vec8) {
   using T = FwdTile<HD>;
-  __shared__ __align__(16) uint8_t smem[T::SMEM];
+  __shared__ __align__(1024) uint8_t kbuf0[T::TILE];
+  __shared__ __align__(1024) uint8_t kbuf1[T::TILE];
+  __shared__ __align__(1024) uint8_t vbuf0[T::TILE];
+  __shared__ __align__(1024) uint8_t vbuf1[T::TILE];
   __shared__ int s_lim[4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hf = lane >> 5, lr = lane & 31;
 
@@ -220,30 +219,28 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
   if (MODE == MODE_BIAS)
     brow = p.bias + (long long)b * p.bsB + (long long)hk * p.bsH + (long long)(rvalid ? r : 0) * p.bsM;
 
-  Staging<HD> st;
+  // ---- pipeline: iteration t reads K(t+1) and V(t) while K(t+2) and V(t+1) stream into the other buffers
+  f32x16_t s_cur[2], s_nxt[2];
   if (t_end > t_beg) {
-    load_tile<HD>(st, Kb, Vb, p.ksM, p.vsM, t_beg * T::BN, kend, tid);
-    store_tile<HD>(st, smem, tid);
+    dma_tile<HD>(kbuf0, Kb, p.ksM, t_beg * T::BN, kend, w, lane);
+    dma_tile<HD>(vbuf0, Vb, p.vsM, t_beg * T::BN, kend, w, lane);
+    if (t_beg + 1 < t_end) dma_tile<HD>(kbuf1, Kb, p.ksM, (t_beg + 1) * T::BN, kend, w, lane);
+    wait_dma_and_sync();
+    if (t_beg * T::BN <= wmax) qk_tile<HD>(s_cur, kbuf0, qf, lr, hf);
+    __syncthreads();  // kbuf0 is refilled in the first iteration
   }
-  __syncthreads();
 
   for (int t = t_beg; t < t_end; ++t) {
-    const int k0 = t * T::BN;
-    if (t + 1 < t_end) load_tile<HD>(st, Kb, Vb, p.ksM, p.vsM, k0 + T::BN, kend, tid);
-    const uint8_t* sb = smem + ((t - t_beg) & 1) * T::STAGE;
+    const int it = t - t_beg, k0 = t * T::BN;
+    uint8_t* kb_next = (it & 1) ? kbuf0 : kbuf1;  // holds K(t+1)
+    uint8_t* kb_fill = (it & 1) ? kbuf1 : kbuf0;  // receives K(t+2)
+    uint8_t* vb_cur = (it & 1) ? vbuf1 : vbuf0;   // holds V(t)
+    uint8_t* vb_fill = (it & 1) ? vbuf0 : vbuf1;  // receives V(t+1)
+    if (t + 2 < t_end) dma_tile<HD>(kb_fill, Kb, p.ksM, k0 + 2 * T::BN, kend, w, lane);
+    if (t + 1 < t_end) dma_tile<HD>(vb_fill, Vb, p.vsM, k0 + T::BN, kend, w, lane);
+    if (t + 1 < t_end && k0 + T::BN <= wmax) qk_tile<HD>(s_nxt, kb_next, qf, lr, hf);
+
     if (k0 <= wmax) {
-      // ---- S^T for 2 blocks of 32 keys: s[kb][v] is key k0 + 32kb + 8(v/4) + 4hf + v%4 of row lr
-      f32x16_t s[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < T::QK; ++ks) {
-          const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(sb + k_off<HD>(32 * kb + lr, 2 * ks + hf));
-          s[kb] = mfma32(as_bf16x8(kf), qf[ks], s[kb]);
-        }
-      }
       if (MODE == MODE_BIAS) {
         // x = (s*scale + bias) * log2(e), bias read only for keys inside the sequence (v8:279-280)
         const float l2e = 1.44269504088896340736f;
@@ -253,48 +250,49 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
           for (int v = 0; v < 16; ++v) {
             const int key = k0 + 32 * kb + 8 * (v >> 2) + 4 * hf + (v & 3);
             const float bv = (rvalid && key < Nb) ? __uint_as_float((uint32_t)brow[key] << 16) : 0.f;
-            s[kb][v] = (s[kb][v] * p.scale + bv) * l2e;
+            s_cur[kb][v] = (s_cur[kb][v] * p.scale + bv) * l2e;
           }
       }
-      if (k0 + T::BN - 1 > wmin) {
+      if (k0 + T::BN - 1 > wmin) {  // the tile straddles some row's last visible key
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const int key = k0 + 32 * kb + 8 * (v >> 2) + 4 * hf + (v & 3);
-            if (key > lim) s[kb][v] = -INFINITY;
+            if (key > lim) s_cur[kb][v] = -INFINITY;
           }
       }
-      // ---- online softmax (log2 domain)
+      // ---- online softmax (log2 domain) with lazy rescaling
       float mx = -INFINITY;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
-      mx = halves_max(mx);
-      const float m_new = fmaxf(m_run, mx * cc);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s_cur[kb][v]);
+      mx = halves_max(mx) * cc;
+      if (__any(mx > m_run + RESCALE_SLACK)) {
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+        m_run = m_new;
+      }
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
       float psum = 0.f;
       uint32_t pk[2][8];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float p0 = fast_exp2(__builtin_fmaf(s[kb][2 * i], cc, -m_use));
-          const float p1 = fast_exp2(__builtin_fmaf(s[kb][2 * i + 1], cc, -m_use));
+          const float p0 = fast_exp2(__builtin_fmaf(s_cur[kb][2 * i], cc, -m_use));
+          const float p1 = fast_exp2(__builtin_fmaf(s_cur[kb][2 * i + 1], cc, -m_use));
           psum += p0;
           psum += p1;
           pk[kb][i] = pack_bf16x2(p0, p1);
         }
-      l_run = l_run * alpha + psum;
-      if (__any(alpha != 1.0f)) {
-#pragma unroll
-        for (int db = 0; db < T::DB; ++db)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
-      }
-      m_run = m_new;
+      l_run += psum;
       // ---- O^T += V^T P^T, 4 MFMA k-steps of 16 keys
 #pragma unroll
       for (int ss = 0; ss < 4; ++ss) {
@@ -302,14 +300,12 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
                             pk[ss >> 1][4 * (ss & 1) + 3]};
         const bf16x8_t pb = as_bf16x8(pw);
 #pragma unroll
-        for (int db = 0; db < T::DB; ++db) {
-          const u32x4_t vf = *reinterpret_cast<const u32x4_t*>(sb + vt_off<HD>(32 * db + lr, 2 * ss + hf));
-          o[db] = mfma32(as_bf16x8(vf), pb, o[db]);
-        }
+        for (int db = 0; db < T::DB; ++db) o[db] = mfma32(v_operand<HD>(vb_cur, db, ss, lane), pb, o[db]);
       }
     }
-    if (t + 1 < t_end) store_tile<HD>(st, smem + ((t + 1 - t_beg) & 1) * T::STAGE, tid);
-    __syncthreads();
+    wait_dma_and_sync();
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) s_cur[kb] = s_nxt[kb];
   }
 
   // ---- epilogue: normalise, LSE, store (O^T layout: lane holds dims 32db + 8(v/4) + 4hf + v%4 of its row)
