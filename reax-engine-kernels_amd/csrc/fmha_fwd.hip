@@ -8,13 +8,14 @@
 //     registers for the whole key loop). The 32x32 accumulator layout then gives lane l the scores of query
 //     l%32 for 16 keys, so the row max / row sum need only in-lane work plus one permlane32 swap.
 //   - The same registers, converted to bf16, are the B operand of O^T = V^T . P^T: no data movement between
-//     the two MFMA stages. The key order inside each 16-key MFMA step is permuted to match the accumulator
-//     layout, and V is stored transposed in LDS in that order so that every A operand is one 16-byte read.
-//   - K/V tiles of 64 keys are double-buffered in LDS (one barrier per tile). K rows use a 16-byte XOR swizzle
-//     (unit ^ (key & 15)); V^T rows use unit ^ ((dim & 7) ^ ((dim >> 3) & 7)): both the MFMA operand reads and
-//     the coalesced global->LDS copies are bank-conflict free.
-//   - Online softmax in base 2 on v_exp_f32 with the running max in log2 units; the O rescale is skipped when
-//     no row of the wavefront raised its max.
+//     the two MFMA stages. The key order inside each 16-key MFMA step follows the accumulator layout, and the
+//     V^T operand is read in that order from the row-major V tile with ds_read_b64_tr_b16 (gfx950's transposing
+//     LDS read).
+//   - K/V tiles of 64 keys stream straight from HBM into LDS (global_load_lds_dwordx4), double-buffered, one
+//     barrier per tile; the S^T of the next tile is computed before the softmax of the current one. Rows use a
+//     16-byte-unit XOR swizzle that keeps both the K operand reads and the transposed V reads bank-conflict free.
+//   - Online softmax in base 2 on v_exp_f32 with the running max in log2 units; the O rescale runs only when a
+//     row max grows by more than 2^8 (probabilities stay <= 2^8).
 //   - Causal / qpos tiles visit only key tiles that some row of the workgroup can see (v8:155-162, 237); the
 //     per-element mask is applied only to tiles that straddle a row's limit. Workgroups are dispatched heaviest
 //     first (v8:134-135) and, when B*H is a multiple of 8, each XCD's L2 serves a fixed set of KV heads.
