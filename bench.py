@@ -60,8 +60,10 @@ def bench_prefill(torch, ops, steps, warmup):
     return cfg, wall, kms
 
 
-def bench_decode(torch, ops, iters):
+def bench_decode(torch, ops, iters, num_splits=None):
     cfg = W.CONFIGS[4]
+    if num_splits:
+        cfg.num_splits = num_splits
     q, k, v, qpos = W.make_decode_inputs(cfg)
     dev = torch.device("cuda:0")
     qd, kd, vd = (W.bits_to_torch(x, dev) for x in (q, k, v))
@@ -144,6 +146,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--only", choices=["prefill", "decode"], help="run one leg only (for profiling)")
+    ap.add_argument("--decode-splits", type=int, default=0, help="override config 4's key-split count")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 5 times: the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -167,8 +170,8 @@ def main():
     from reax_fmha import ops
 
     if args.only == "decode":
-        dcfg, dms, gbs = bench_decode(torch, ops, args.steps)
-        print(json.dumps({"decode_GBs": round(gbs, 1), "ms": round(dms, 4)}), flush=True)
+        dcfg, dms, gbs = bench_decode(torch, ops, args.steps, args.decode_splits)
+        print(json.dumps({"decode_GBs": round(gbs, 1), "ms": round(dms, 4), "splits": dcfg.num_splits}), flush=True)
         return
     cfg, wall, kms = bench_prefill(torch, ops, args.steps, args.warmup)
     if args.only == "prefill":

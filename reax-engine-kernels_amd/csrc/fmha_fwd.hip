@@ -23,6 +23,7 @@
 #include "fmha_launch.h"
 
 #include <climits>
+#include <type_traits>
 
 namespace reax {
 
@@ -40,10 +41,12 @@ struct FwdTile {
   static_assert(HD == 128 || HD == 256, "head_dim 128 or 256");
 };
 
-// Row-major K/V tiles with a 16-byte-unit XOR swizzle. For 8 consecutive rows f() takes 8 distinct values
-// (conflict-free 16-byte K operand reads of 8 rows at one unit), and for 4 consecutive rows f()/2 takes 4
-// distinct values (conflict-free transposed V reads: 4 rows x 2 adjacent units per 16-lane group).
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1) | (r & 8); }
+// Row-major K/V tiles with a 16-byte-unit XOR swizzle for gfx950's 64-bank LDS (256 bytes per access phase):
+//   - K operand reads (ds_read_b128, 16 lanes per phase) touch 16 consecutive rows at one unit: f() is a
+//     bijection on r mod 16, so the 16 units land in 16 distinct bank groups;
+//   - transposed V reads (ds_read_b64_tr_b16, 32 lanes per phase) touch 4 consecutive rows x 4 adjacent units:
+//     bits 2-3 of f() (= r & 3) differ across the 4 rows, so the 16 (row, unit) pieces are distinct.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 template <int HD>
 __device__ __forceinline__ uint32_t tile_off(int r, int u) {
   return (uint32_t)(r * (HD * 2) + ((u ^ swz(r)) << 4));
@@ -53,41 +56,93 @@ __device__ __forceinline__ u32x4_t ld16(const uint16_t* p) { return *reinterpret
 
 #define REAX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
-// Direct global -> LDS copy of the K or V tile at key k0 into `buf` (this wavefront's share). Lane l of load c
-// fills bytes [c*1024 + 16 l, +16) of the tile, i.e. row r, swizzled unit pu; it fetches the logical unit that
-// belongs there. Keys past the window are clamped to its last key: their scores are masked, so they only ever
-// meet a zero probability.
-template <int HD>
-__device__ __forceinline__ void dma_tile(uint8_t* buf, const uint16_t* base, long long stride, int k0, int kend,
-                                         int w, int lane) {
-  using T = FwdTile<HD>;
-#pragma unroll
-  for (int i = 0; i < T::DMA_W; ++i) {
-    const int c = w * T::DMA_W + i;
-    const int byte = c * 1024 + 16 * lane;
-    const int r = byte / (HD * 2), pu = (byte % (HD * 2)) >> 4;
-    const int u = pu ^ swz(r);
-    const int key = min(k0 + r, kend - 1);
-    __builtin_amdgcn_global_load_lds(base + (long long)key * stride + 8 * u, REAX_LDS(buf + c * 1024), 16, 0, 0);
-  }
+// One 16-byte direct global -> LDS load per lane (global_load_lds_dwordx4): lane l's bytes land at lds + 16 l.
+__device__ __forceinline__ void lds_dma16(const void* src, uint8_t* lds) {
+  __builtin_amdgcn_global_load_lds(src, REAX_LDS(lds), 16, 0, 0);
 }
+
+// Direct global -> LDS copy of a K or V tile. Load c of a tile fills bytes [c*1024, c*1024 + 1024): lane l
+// lands at c*1024 + 16 l, i.e. row r, swizzled unit pu, and fetches the logical unit u = pu ^ swz(r) of that
+// row. With NWV wavefronts per workgroup, wavefront w issues loads c = w*DW .. w*DW + DW - 1 (DW = DMA / NWV).
+template <int HD, int NWV>
+struct Dma {
+  static constexpr int DW = FwdTile<HD>::DMA / NWV;
+  static_assert(DW >= 1 && DW * NWV == FwdTile<HD>::DMA, "tile loads split evenly over the wavefronts");
+  uint32_t off[DW];  // byte offset of this lane's source relative to the tile's first key row
+
+  __device__ __forceinline__ static void slot(int w, int i, int lane, int& r, int& u) {
+    const int byte = (w * DW + i) * 1024 + 16 * lane;
+    r = byte / (HD * 2);
+    u = ((byte % (HD * 2)) >> 4) ^ swz(r);
+  }
+  __device__ __forceinline__ Dma(long long stride, int w, int lane) {
+#pragma unroll
+    for (int i = 0; i < DW; ++i) {
+      int r, u;
+      slot(w, i, lane, r, u);
+      off[i] = (uint32_t)((long long)r * stride * 2 + 16 * u);
+    }
+  }
+  // Copies the tile at key k0. Full tiles (k0 + BN <= kend, and 32-bit row offsets) use the precomputed
+  // offsets; a partial last tile clamps its rows to the window's last key: those scores are masked, so they
+  // only ever meet a zero probability.
+  __device__ __forceinline__ void tile(uint8_t* buf, const uint16_t* base, long long stride, bool fast, int k0,
+                                       int kend, int w, int lane) const {
+    if (fast && k0 + FwdTile<HD>::BN <= kend) {
+      const uint16_t* tb = base + (long long)k0 * stride;
+#pragma unroll
+      for (int i = 0; i < DW; ++i)
+        lds_dma16(reinterpret_cast<const uint8_t*>(tb) + off[i], buf + (w * DW + i) * 1024);
+    } else {
+#pragma unroll
+      for (int i = 0; i < DW; ++i) {
+        int r, u;
+        slot(w, i, lane, r, u);
+        const int key = min(k0 + r, kend - 1);
+        lds_dma16(base + (long long)key * stride + 8 * u, buf + (w * DW + i) * 1024);
+      }
+    }
+  }
+};
 
 __device__ __forceinline__ void wait_dma_and_sync() {
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's direct-to-LDS loads have landed
   __syncthreads();                     // ... and every other wavefront's
 }
 
+// LDS read addresses. Row offsets (multiples of HD*2) and the swizzled 16-byte unit (bits 4..8) occupy disjoint
+// bits, so every operand address is a per-lane base XOR a compile-time constant (plus a constant offset).
+//   K operand (kb, ks): row 32kb + lr, unit 2ks + hf  ->  kbase[kb] ^ (32 ks)
+//   V operand (db, ss, second half): row 16ss + 4h + i/4 + 8*second, unit 4db + 2dh + (i&3)/2, byte 8(i&1)
+//     -> (16ss + 8 second)*HD*2 + (vbase ^ vconst(db, second))
+template <int HD>
+__device__ __forceinline__ uint32_t k_lane_base(int kb, int lr, int hf) {
+  const int r = 32 * kb + lr;
+  return (uint32_t)(r * HD * 2 + ((hf ^ swz(r)) << 4));
+}
+// With row = 16ss + 4h + i/4 + 8 second, swz(row) = ((i/4) << 2) | h | (second << 1) and the unit is
+// 4db + 2dh + (i&3)/2, so unit ^ swz(row) = L(lane) ^ C(db, second) with the two parts below.
+template <int HD>
+__device__ __forceinline__ uint32_t v_lane_base(int lane) {
+  const int h = lane >> 5, dh = (lane >> 4) & 1, i = lane & 15;
+  const int L = (((i >> 1) & 1) ^ h) | (dh << 1) | (((i >> 2) & 3) << 2);
+  return (uint32_t)((4 * h + (i >> 2)) * HD * 2 + (L << 4) + 8 * (i & 1));
+}
+__device__ __forceinline__ constexpr uint32_t v_const(int db, int second) {
+  return (uint32_t)(((second << 1) | ((db & 3) << 2) | (((db >> 2) & 1) << 4)) << 4);
+}
+
 // S^T for one 64-key tile: s[kb][v] = score of this lane's row against key 32kb + 8(v/4) + 4hf + v%4.
 template <int HD>
-__device__ __forceinline__ void qk_tile(f32x16_t (&s)[2], const uint8_t* kb_, const bf16x8_t (&qf)[HD / 16], int lr,
-                                        int hf) {
+__device__ __forceinline__ void qk_tile(f32x16_t (&s)[2], const uint8_t* kbuf, const bf16x8_t (&qf)[HD / 16],
+                                        const uint32_t (&kbase)[2]) {
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) {
-      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb_ + tile_off<HD>(32 * kb + lr, 2 * ks + hf));
+      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kbuf + (kbase[kb] ^ (32u * ks)));
       s[kb] = mfma32(as_bf16x8(kf), qf[ks], s[kb]);
     }
   }
@@ -95,20 +150,19 @@ __device__ __forceinline__ void qk_tile(f32x16_t (&s)[2], const uint8_t* kb_, co
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
+__device__ __forceinline__ u32x2_t ds_read_tr16(const uint8_t* p) {
+  const i16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(p));
+  return __builtin_bit_cast(u32x2_t, a);
+}
+
 // V^T operand (32 dims x 16 keys in MFMA key order) of dim block db, k-step ss, from the row-major V tile with
-// two ds_read_b64_tr_b16: in each 16-lane group, lane i reads 4 dims of key row (i/4) and receives 4 keys of
-// dim (i%16) back.
+// two ds_read_b64_tr_b16: in each 16-lane group, lane i reads 4 dims of key row i/4 and receives 4 keys of
+// dim i back.
 template <int HD>
-__device__ __forceinline__ bf16x8_t v_operand(const uint8_t* vb, int db, int ss, int lane) {
-  const int h = lane >> 5, dh = (lane >> 4) & 1, i = lane & 15;
-  const int row = 16 * ss + 4 * h + (i >> 2);
-  const int u = 4 * db + 2 * dh + ((i & 3) >> 1);
-  const uint8_t* p0 = vb + tile_off<HD>(row, u) + 8 * (i & 1);
-  const uint8_t* p1 = vb + tile_off<HD>(row + 8, u) + 8 * (i & 1);
-  const i16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(p0));
-  const i16x4_t b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(p1));
-  const u32x2_t ua = __builtin_bit_cast(u32x2_t, a), ub = __builtin_bit_cast(u32x2_t, b);
-  return as_bf16x8(u32x4_t{ua[0], ua[1], ub[0], ub[1]});
+__device__ __forceinline__ bf16x8_t v_operand(const uint8_t* vbuf, int db, int ss, uint32_t vbase) {
+  const u32x2_t a = ds_read_tr16(vbuf + 16 * ss * HD * 2 + (vbase ^ v_const(db, 0)));
+  const u32x2_t b = ds_read_tr16(vbuf + (16 * ss + 8) * HD * 2 + (vbase ^ v_const(db, 1)));
+  return as_bf16x8(u32x4_t{a[0], a[1], b[0], b[1]});
 }
 
 __device__ __forceinline__ int wave_max(int x) {
@@ -221,26 +275,29 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
     brow = p.bias + (long long)b * p.bsB + (long long)hk * p.bsH + (long long)(rvalid ? r : 0) * p.bsM;
 
   // ---- pipeline: iteration t reads K(t+1) and V(t) while K(t+2) and V(t+1) stream into the other buffers
-  f32x16_t s_cur[2], s_nxt[2];
+  const Dma<HD, 4> kplan(p.ksM, w, lane), vplan(p.vsM, w, lane);
+  const bool kfast = p.ksM * 2 * T::BN < (1ll << 31), vfast = p.vsM * 2 * T::BN < (1ll << 31);
+  const uint32_t kbase[2] = {k_lane_base<HD>(0, lr, hf), k_lane_base<HD>(1, lr, hf)};
+  const uint32_t vbase = v_lane_base<HD>(lane);
+  f32x16_t sa[2];
   if (t_end > t_beg) {
-    dma_tile<HD>(kbuf0, Kb, p.ksM, t_beg * T::BN, kend, w, lane);
-    dma_tile<HD>(vbuf0, Vb, p.vsM, t_beg * T::BN, kend, w, lane);
-    if (t_beg + 1 < t_end) dma_tile<HD>(kbuf1, Kb, p.ksM, (t_beg + 1) * T::BN, kend, w, lane);
+    kplan.tile(kbuf0, Kb, p.ksM, kfast, t_beg * T::BN, kend, w, lane);
+    vplan.tile(vbuf0, Vb, p.vsM, vfast, t_beg * T::BN, kend, w, lane);
+    if (t_beg + 1 < t_end) kplan.tile(kbuf1, Kb, p.ksM, kfast, (t_beg + 1) * T::BN, kend, w, lane);
     wait_dma_and_sync();
-    if (t_beg * T::BN <= wmax) qk_tile<HD>(s_cur, kbuf0, qf, lr, hf);
+    if (t_beg * T::BN <= wmax) qk_tile<HD>(sa, kbuf0, qf, kbase);
     __syncthreads();  // kbuf0 is refilled in the first iteration
   }
 
-  for (int t = t_beg; t < t_end; ++t) {
-    const int it = t - t_beg, k0 = t * T::BN;
-    uint8_t* kb_next = (it & 1) ? kbuf0 : kbuf1;  // holds K(t+1)
-    uint8_t* kb_fill = (it & 1) ? kbuf1 : kbuf0;  // receives K(t+2)
-    uint8_t* vb_cur = (it & 1) ? vbuf1 : vbuf0;   // holds V(t)
-    uint8_t* vb_fill = (it & 1) ? vbuf0 : vbuf1;  // receives V(t+1)
-    if (t + 2 < t_end) dma_tile<HD>(kb_fill, Kb, p.ksM, k0 + 2 * T::BN, kend, w, lane);
-    if (t + 1 < t_end) dma_tile<HD>(vb_fill, Vb, p.vsM, k0 + T::BN, kend, w, lane);
-    if (t + 1 < t_end && k0 + T::BN <= wmax) qk_tile<HD>(s_nxt, kb_next, qf, lr, hf);
-
+  // One pipeline step on tile t: s_cur holds S(t), s_nxt receives S(t+1); kb_next holds K(t+1), vb_cur V(t),
+  // while kb_fill / vb_fill receive K(t+2) / V(t+1). The loop below is unrolled by two so the score buffers and
+  // LDS buffers swap roles at compile time (no register copies, constant LDS addresses).
+  auto step = [&](int t, f32x16_t(&s_cur)[2], f32x16_t(&s_nxt)[2], const uint8_t* kb_next, uint8_t* kb_fill,
+                  const uint8_t* vb_cur, uint8_t* vb_fill) {
+    const int k0 = t * T::BN;
+    if (t + 2 < t_end) kplan.tile(kb_fill, Kb, p.ksM, kfast, k0 + 2 * T::BN, kend, w, lane);
+    if (t + 1 < t_end) vplan.tile(vb_fill, Vb, p.vsM, vfast, k0 + T::BN, kend, w, lane);
+    const bool nxt = t + 1 < t_end && k0 + T::BN <= wmax;
     if (k0 <= wmax) {
       if (MODE == MODE_BIAS) {
         // x = (s*scale + bias) * log2(e), bias read only for keys inside the sequence (v8:279-280)
@@ -281,32 +338,57 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
         m_run = m_new;
       }
       const float m_use = m_run == -INFINITY ? 0.f : m_run;
-      float psum = 0.f;
-      uint32_t pk[2][8];
+      // straight-line block: S(t+1) MFMAs interleaved with the exponentials of tile t, then O += V(t)^T P^T
+      auto body = [&](auto with_next) __attribute__((always_inline)) {
+        constexpr bool NEXT = decltype(with_next)::value;
+        float psum = 0.f;
+        uint32_t pk[2][8];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float p0 = fast_exp2(__builtin_fmaf(s_cur[kb][2 * i], cc, -m_use));
-          const float p1 = fast_exp2(__builtin_fmaf(s_cur[kb][2 * i + 1], cc, -m_use));
-          psum += p0;
-          psum += p1;
-          pk[kb][i] = pack_bf16x2(p0, p1);
+          for (int i = 0; i < 8; ++i) {
+            const float p0 = fast_exp2(__builtin_fmaf(s_cur[kb][2 * i], cc, -m_use));
+            const float p1 = fast_exp2(__builtin_fmaf(s_cur[kb][2 * i + 1], cc, -m_use));
+            psum += p0;
+            psum += p1;
+            pk[kb][i] = pack_bf16x2(p0, p1);
+          }
+        l_run += psum;
+#pragma unroll
+        for (int ss = 0; ss < 4; ++ss) {
+          const u32x4_t pw = {pk[ss >> 1][4 * (ss & 1) + 0], pk[ss >> 1][4 * (ss & 1) + 1],
+                              pk[ss >> 1][4 * (ss & 1) + 2], pk[ss >> 1][4 * (ss & 1) + 3]};
+          const bf16x8_t pb = as_bf16x8(pw);
+#pragma unroll
+          for (int db = 0; db < T::DB; ++db) o[db] = mfma32(v_operand<HD>(vb_cur, db, ss, vbase), pb, o[db]);
         }
-      l_run += psum;
-      // ---- O^T += V^T P^T, 4 MFMA k-steps of 16 keys
+        if (NEXT) {
 #pragma unroll
-      for (int ss = 0; ss < 4; ++ss) {
-        const u32x4_t pw = {pk[ss >> 1][4 * (ss & 1) + 0], pk[ss >> 1][4 * (ss & 1) + 1], pk[ss >> 1][4 * (ss & 1) + 2],
-                            pk[ss >> 1][4 * (ss & 1) + 3]};
-        const bf16x8_t pb = as_bf16x8(pw);
+          for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int db = 0; db < T::DB; ++db) o[db] = mfma32(v_operand<HD>(vb_cur, db, ss, lane), pb, o[db]);
-      }
+            for (int e = 0; e < 16; ++e) s_nxt[kb][e] = 0.f;
+#pragma unroll
+          for (int ks = 0; ks < T::QK; ++ks)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+              const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb_next + (kbase[kb] ^ (32u * ks)));
+              s_nxt[kb] = mfma32(as_bf16x8(kf), qf[ks], s_nxt[kb]);
+            }
+        }
+      };
+      if (nxt)
+        body(std::integral_constant<bool, true>{});
+      else
+        body(std::integral_constant<bool, false>{});
+    } else if (nxt) {
+      qk_tile<HD>(s_nxt, kb_next, qf, kbase);
     }
     wait_dma_and_sync();
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) s_cur[kb] = s_nxt[kb];
+  };
+
+  for (int t = t_beg; t < t_end; t += 2) {
+    step(t, sa, sa, kbuf1, kbuf0, vbuf0, vbuf1);
+    if (t + 1 < t_end) step(t + 1, sa, sa, kbuf0, kbuf1, vbuf1, vbuf0);
   }
 
   // ---- epilogue: normalise, LSE, store (O^T layout: lane holds dims 32db + 8(v/4) + 4hf + v%4 of its row)
@@ -355,6 +437,251 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
         *reinterpret_cast<u32x2_t*>(orow + d) = res;
       }
     return;
+  }
+  if (!p.o) return;
+  uint16_t* orow = p.o + (long long)b * p.osB + (long long)hk * p.osH + (tok0 + tok) * p.osT + (long long)g * p.osG;
+#pragma unroll
+  for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = 32 * db + 8 * q4 + 4 * hf;
+      const uint32_t w0 = pack_bf16x2(o[db][4 * q4 + 0] * inv, o[db][4 * q4 + 1] * inv);
+      const uint32_t w1 = pack_bf16x2(o[db][4 * q4 + 2] * inv, o[db][4 * q4 + 3] * inv);
+      if (o_vec8) {
+        *reinterpret_cast<u32x2_t*>(orow + d) = u32x2_t{w0, w1};
+      } else {
+        *reinterpret_cast<uint32_t*>(orow + d) = w0;
+        *reinterpret_cast<uint32_t*>(orow + d + 2) = w1;
+      }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// Ping-pong forward for head_dim 128 (qpos / varlen, O + LSE): 8 wavefronts = 256 folded rows per workgroup.
+// Wavefronts w and w + 4 run on the same SIMD (the dispatcher deals a workgroup's wavefronts round-robin over the
+// CU's 4 SIMDs), so the workgroup is split into group 0 (w < 4, rows 0..127) and group 1 (w >= 4, rows
+// 128..255) that alternate phases at every half-step barrier:
+//     half 1 of step t: group 0 runs its MFMA phase  [P(t-1).V(t-1), then S(t) = K(t).Q^T]
+//                       group 1 runs its VALU phase  [softmax of S(t-1) -> P(t-1)]
+//     half 2 of step t: the roles swap.
+// While one wavefront of a SIMD keeps the matrix core busy, the other one does its exponentials, so the
+// MFMA pipe never waits for a softmax. K(t+1) and V(t) stream into LDS during step t (two buffers each).
+constexpr int PP_NW = 8;
+#ifndef REAX_PP_STAGES
+#define REAX_PP_STAGES 2
+#endif
+constexpr int PP_BM = 256;
+
+template <int MODE, int NS>
+__global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, int o_vec8) {
+  constexpr int HD = 128;
+  using T = FwdTile<HD>;
+  static_assert(NS >= 2 && NS <= 4, "2..4 K/V stages");
+  __shared__ __align__(1024) uint8_t kring[NS][T::TILE];
+  __shared__ __align__(1024) uint8_t vring[NS][T::TILE];
+  __shared__ int s_lim[PP_NW];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hf = lane >> 5, lr = lane & 31;
+  const int grp = w >> 2;
+
+  // ---- workgroup -> (batch, KV head, row tile): heaviest tile first; XCD-aware when B*H % 8 == 0
+  const int BH = p.B * p.H, id = blockIdx.x;
+  int bh, rank;
+  if ((BH & 7) == 0) {
+    const int per = BH >> 3, x = id & 7, j = id >> 3;
+    bh = x + 8 * (j % per);
+    rank = j / per;
+  } else {
+    bh = id % BH;
+    rank = id / BH;
+  }
+  const int tile = p.n_tiles - 1 - rank;
+  const int b = bh / p.H, hk = bh - b * p.H;
+  long long tok0 = 0;
+  int Mb = p.M, Nb = p.N;
+  if (MODE == MODE_VARLEN) {
+    const int s0 = p.cu_seqlens[b], s1 = p.cu_seqlens[b + 1];
+    tok0 = s0;
+    Nb = s1 - s0;
+    Mb = Nb * p.G;
+  }
+  const int r0 = tile * PP_BM;
+  if (r0 >= Mb) return;  // uniform over the workgroup
+
+  const int r = r0 + 32 * w + lr;
+  const bool rvalid = r < Mb;
+  const int tok = rvalid ? r / p.G : 0;
+  const int g = rvalid ? r - tok * p.G : 0;
+  int lim = -1;
+  if (rvalid) {
+    lim = MODE == MODE_QPOS ? min(p.qpos[(long long)b * p.qpBs + tok], Nb - 1) : min(tok, Nb - 1);
+    lim = max(lim, -1);
+  }
+  const int wmax = wave_max(lim), wmin = wave_min(lim);
+  if (lane == 0) s_lim[w] = wmax;
+  __syncthreads();
+  int cmax = s_lim[0];
+#pragma unroll
+  for (int i = 1; i < PP_NW; ++i) cmax = max(cmax, s_lim[i]);
+  const int t_end = cmax < 0 ? 0 : cmax / T::BN + 1;
+
+  const uint16_t* qrow = p.q + (long long)b * p.qsB + (long long)hk * p.qsH + (tok0 + tok) * p.qsT + (long long)g * p.qsG;
+  bf16x8_t qf[T::QK];
+#pragma unroll
+  for (int ks = 0; ks < T::QK; ++ks)
+    qf[ks] = as_bf16x8(rvalid ? ld16(qrow + 16 * ks + 8 * hf) : u32x4_t{0u, 0u, 0u, 0u});
+  const uint16_t* Kb = p.k + (long long)b * p.ksB + (long long)hk * p.ksH + tok0 * p.ksM;
+  const uint16_t* Vb = p.v + (long long)b * p.vsB + (long long)hk * p.vsH + tok0 * p.vsM;
+
+  f32x16_t o[T::DB];
+#pragma unroll
+  for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const float cc = p.scale_log2;
+  f32x16_t s[2];
+  uint32_t pk[2][8];
+
+  const Dma<HD, PP_NW> kplan(p.ksM, w, lane), vplan(p.vsM, w, lane);
+  const bool kfast = p.ksM * 2 * T::BN < (1ll << 31), vfast = p.vsM * 2 * T::BN < (1ll << 31);
+  const uint32_t kbase[2] = {k_lane_base<HD>(0, lr, hf), k_lane_base<HD>(1, lr, hf)};
+  const uint32_t vbase = v_lane_base<HD>(lane);
+
+  // softmax of tile t: S in s[] -> P in pk[] (bf16), running max / row sum, lazy O rescale
+  auto softmax = [&](int t) __attribute__((always_inline)) {
+    const int k0 = t * T::BN;
+    if (k0 > wmax) return;
+    if (k0 + T::BN - 1 > wmin) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = k0 + 32 * kb + 8 * (v >> 2) + 4 * hf + (v & 3);
+          if (key > lim) s[kb][v] = -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
+    mx = halves_max(mx) * cc;
+    if (__any(mx > m_run + RESCALE_SLACK)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p0 = fast_exp2(__builtin_fmaf(s[kb][2 * i], cc, -m_use));
+        const float p1 = fast_exp2(__builtin_fmaf(s[kb][2 * i + 1], cc, -m_use));
+        psum += p0;
+        psum += p1;
+        pk[kb][i] = pack_bf16x2(p0, p1);
+      }
+    l_run += psum;
+  };
+  // MFMA phase of step t: O += V(t-1)^T P(t-1)^T, then S(t) = K(t) Q^T. When both halves run (the common
+  // case) they form one straight-line block whose order is pinned: LDS operand reads run four MFMAs ahead of
+  // their use, so the matrix core never waits for LDS.
+  auto pv_part = [&](const uint8_t* vb_prev) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ss = 0; ss < 4; ++ss) {
+      const u32x4_t pw = {pk[ss >> 1][4 * (ss & 1) + 0], pk[ss >> 1][4 * (ss & 1) + 1],
+                          pk[ss >> 1][4 * (ss & 1) + 2], pk[ss >> 1][4 * (ss & 1) + 3]};
+      const bf16x8_t pb = as_bf16x8(pw);
+#pragma unroll
+      for (int db = 0; db < T::DB; ++db) o[db] = mfma32(v_operand<HD>(vb_prev, db, ss, vbase), pb, o[db]);
+    }
+  };
+  auto mfma_phase = [&](int t, const uint8_t* kb_t, const uint8_t* vb_prev) __attribute__((always_inline)) {
+    const bool pv = t >= 1 && (t - 1) * T::BN <= wmax;
+    const bool qk = t < t_end && t * T::BN <= wmax;
+    if (pv && qk) {
+      pv_part(vb_prev);
+      qk_tile<HD>(s, kb_t, qf, kbase);
+      // pinned order: 8 V reads, then 16 x [PV MFMA, 2 reads], then 16 x [QK MFMA, 1 read]
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    } else if (pv) {
+      pv_part(vb_prev);
+    } else if (qk) {
+      qk_tile<HD>(s, kb_t, qf, kbase);
+    }
+  };
+
+  if (t_end > 0) {
+    // ring of NS stages: step t reads K(t) from kring[t % NS] and V(t-1) from vring[(t-1) % NS]; it fills
+    // kring[(t-1) % NS] with K(t+NS-1) and vring[(t-2) % NS] with V(t+NS-2), whose previous contents were
+    // last read in step t-1. Each step waits only for the loads issued NS-2 steps earlier.
+    constexpr int PER_STEP = 2 * Dma<HD, PP_NW>::DW;  // loads per wavefront per step
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j)
+      if (j < t_end) kplan.tile(kring[j], Kb, p.ksM, kfast, j * T::BN, Nb, w, lane);
+#pragma unroll
+    for (int j = 0; j < NS - 2; ++j)
+      if (j < t_end) vplan.tile(vring[j], Vb, p.vsM, vfast, j * T::BN, Nb, w, lane);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // all prologue loads (simplest: the first step needs K(0) anyway)
+    __syncthreads();
+    auto step = [&](int t, const uint8_t* kb_t, uint8_t* kb_fill, const uint8_t* vb_prev, uint8_t* vb_fill) __attribute__((always_inline)) {
+      if (t + NS - 1 < t_end) kplan.tile(kb_fill, Kb, p.ksM, kfast, (t + NS - 1) * T::BN, Nb, w, lane);
+      if (t + NS - 2 < t_end) vplan.tile(vb_fill, Vb, p.vsM, vfast, (t + NS - 2) * T::BN, Nb, w, lane);
+      if (grp == 0)
+        mfma_phase(t, kb_t, vb_prev);
+      else if (t >= 1)
+        softmax(t - 1);
+      __syncthreads();
+      if (grp == 0) {
+        if (t < t_end) softmax(t);
+      } else {
+        mfma_phase(t, kb_t, vb_prev);
+      }
+      // K(t+1) and V(t) must have landed: they were issued NS-2 steps ago (or in the prologue), and loads return
+      // in issue order, so vmcnt((NS-2) * PER_STEP) leaves exactly the loads of the last NS-2 steps in flight.
+      // That count is only right while every one of those steps issued its full PER_STEP loads, which holds
+      // iff this step still issued a K load; near the end of the loop everything is drained instead.
+      if (NS == 2 || t + NS - 1 >= t_end) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+      } else if (NS == 3) {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | PER_STEP);
+      } else {
+        __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * PER_STEP));
+      }
+      __syncthreads();
+    };
+    for (int t = 0; t <= t_end; t += NS) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j)
+        if (t + j <= t_end)
+          step(t + j, kring[j], kring[(j + NS - 1) % NS], vring[(j + NS - 1) % NS], vring[(j + NS - 2) % NS]);
+    }
+  }
+
+  // ---- epilogue: normalise, LSE, store
+  const float l = halves_sum(l_run);
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  if (!rvalid) return;
+  if (p.lse && hf == 0) {
+    const float lse = l > 0.f ? (m_run + log2f(l)) * 0.69314718055994530942f : -INFINITY;
+    p.lse[(long long)b * p.lsB + (long long)hk * p.lsH + (tok0 + tok) * p.lsT + (long long)g * p.lsG] = lse;
   }
   if (!p.o) return;
   uint16_t* orow = p.o + (long long)b * p.osB + (long long)hk * p.osH + (tok0 + tok) * p.osT + (long long)g * p.osG;
@@ -451,9 +778,25 @@ static int prepare(FwdParams& p, bool post) {
   return 0;
 }
 
+template <int MODE>
+static int launch_fwd_pp(FwdParams p, hipStream_t stream) {
+  p.n_tiles = (int)(((long long)p.M + PP_BM - 1) / PP_BM);
+  const long long nwg = (long long)p.B * p.H * p.n_tiles;
+  if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  const int o_vec8 = p.o ? (aligned_elems(p.o, 4, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0) : 0;
+  hipLaunchKernelGGL((fmha_fwd_pp_kernel<MODE, REAX_PP_STAGES>), dim3((unsigned)nwg), dim3(64 * PP_NW), 0, stream, p, o_vec8);
+  return (int)hipGetLastError();
+}
+
 int launch_fwd(const FwdParams& p0, int head_dim, int mode, bool post, hipStream_t stream) {
   FwdParams p = p0;
   if (const int rc = prepare(p, post)) return rc;
+  // head_dim 128 qpos / varlen without the POST epilogue: the ping-pong kernel once a row tile has enough rows
+  // to fill both groups (short query blocks, e.g. decode, keep the 4-wavefront kernel)
+  if (head_dim == 128 && !post && p.M > FwdTile<128>::BM) {
+    if (mode == MODE_QPOS) return launch_fwd_pp<MODE_QPOS>(p, stream);
+    if (mode == MODE_VARLEN) return launch_fwd_pp<MODE_VARLEN>(p, stream);
+  }
   if (head_dim == 128) {
     if (mode == MODE_QPOS)
       return post ? launch_fwd_t<128, MODE_QPOS, true, false>(p, stream) : launch_fwd_t<128, MODE_QPOS, false, false>(p, stream);
