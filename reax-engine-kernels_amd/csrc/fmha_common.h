@@ -65,6 +65,10 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
 }
 
+// s_waitcnt immediate that waits until at most n (< 64) vector-memory loads of this wavefront are outstanding and
+// leaves the export and LDS/scalar counters unconstrained (vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8])
+constexpr int vmcnt_le(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Combine a value with the one held 32 lanes away (the other half of the wavefront). v_permlane32_swap

@@ -61,6 +61,17 @@ __device__ __forceinline__ void lds_dma16(const void* src, uint8_t* lds) {
   __builtin_amdgcn_global_load_lds(src, REAX_LDS(lds), 16, 0, 0);
 }
 
+// The same load issued as inline assembly with the nontemporal hint, for data read exactly once (the K/V stream of
+// a decode step): measured on MI355X, a cold streaming read with nt runs at ~6.8 TB/s against ~3.9 TB/s without
+// it when the caches hold dirty lines. The compiler keeps no direct-to-LDS bookkeeping for inline assembly, so it
+// adds no conservative vmcnt(0) before later LDS reads of other buffers; the caller orders the load explicitly:
+// s_waitcnt vmcnt before reading the destination, lgkmcnt(0) after the last read of a region before loading into
+// it again.
+__device__ __forceinline__ void lds_dma16_stream(const void* src, uint8_t* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(lds));
+  asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(src), "{m0}"(m0) : "memory");
+}
+
 // Direct global -> LDS copy of a K or V tile. Load c of a tile fills bytes [c*1024, c*1024 + 1024): lane l
 // lands at c*1024 + 16 l, i.e. row r, swizzled unit pu, and fetches the logical unit u = pu ^ swz(r) of that
 // row. With NWV wavefronts per workgroup, wavefront w issues loads c = w*DW .. w*DW + DW - 1 (DW = DMA / NWV).
@@ -86,20 +97,29 @@ struct Dma {
   // Copies the tile at key k0. Full tiles (k0 + BN <= kend, and 32-bit row offsets) use the precomputed
   // offsets; a partial last tile clamps its rows to the window's last key: those scores are masked, so they
   // only ever meet a zero probability.
+  template <bool STREAM = false>
   __device__ __forceinline__ void tile(uint8_t* buf, const uint16_t* base, long long stride, bool fast, int k0,
                                        int kend, int w, int lane) const {
     if (fast && k0 + FwdTile<HD>::BN <= kend) {
       const uint16_t* tb = base + (long long)k0 * stride;
 #pragma unroll
-      for (int i = 0; i < DW; ++i)
-        lds_dma16(reinterpret_cast<const uint8_t*>(tb) + off[i], buf + (w * DW + i) * 1024);
+      for (int i = 0; i < DW; ++i) {
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(tb) + off[i];
+        if (STREAM)
+          lds_dma16_stream(src, buf + (w * DW + i) * 1024);
+        else
+          lds_dma16(src, buf + (w * DW + i) * 1024);
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < DW; ++i) {
         int r, u;
         slot(w, i, lane, r, u);
         const int key = min(k0 + r, kend - 1);
-        lds_dma16(base + (long long)key * stride + 8 * u, buf + (w * DW + i) * 1024);
+        if (STREAM)
+          lds_dma16_stream(base + (long long)key * stride + 8 * u, buf + (w * DW + i) * 1024);
+        else
+          lds_dma16(base + (long long)key * stride + 8 * u, buf + (w * DW + i) * 1024);
       }
     }
   }
@@ -661,9 +681,9 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
       if (NS == 2 || t + NS - 1 >= t_end) {
         __builtin_amdgcn_s_waitcnt(0x0F70);
       } else if (NS == 3) {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | PER_STEP);
+        __builtin_amdgcn_s_waitcnt(vmcnt_le(PER_STEP));
       } else {
-        __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * PER_STEP));
+        __builtin_amdgcn_s_waitcnt(vmcnt_le(2 * PER_STEP));
       }
       __syncthreads();
     };
@@ -701,11 +721,199 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
     }
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// Split-KV decode for short query blocks (head_dim 128, at most 32 folded rows per (b, KV head)). The key range of
+// each (b, KV head) is cut into num_splits splits of split_len keys; each split is streamed by P = 1, 2 or 4
+// wavefronts (p.wpsplit), each over its own part of split_len / P keys (a whole number of 64-key tiles) through a
+// private LDS region (a K and a V tile), so the loop has no workgroup barrier: the next K tile loads while the
+// softmax and P.V of the current tile run, the next V tile while the next S^T runs. All G query heads of the KV
+// head share each K/V tile. A workgroup's 4 wavefronts take 4 / P consecutive (b, split, KV head) tasks, KV head
+// fastest, so with P = 1 they read neighbouring 256-byte head slices of the same cache rows together. At the end
+// the P partials of a split merge through LDS into the split's partial (O / l in fp32 and its natural-log LSE),
+// which splitkv_combine_kernel merges across splits.
+constexpr int DEC_NW = 4;
+
+template <int HD>
+__global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, int wpsplit) {
+  using T = FwdTile<HD>;
+  static_assert(HD == 128, "the decode kernel keeps 2 x 16 KB of LDS per wavefront");
+  __shared__ __align__(1024) uint8_t kbuf[DEC_NW][T::TILE];
+  __shared__ __align__(1024) uint8_t vbuf[DEC_NW][T::TILE];
+  const int tid = threadIdx.x, lane = tid & 63, hf = lane >> 5, lr = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wavefront-uniform: keeps the loop control scalar
+  const int P = wpsplit, part = w % P;
+  const long long ntask = (long long)p.B * p.num_splits * p.H;
+  const long long task = (long long)blockIdx.x * (DEC_NW / P) + w / P;
+  const bool active = task < ntask;
+  const long long tk = active ? task : 0;
+  const int hk = (int)(tk % p.H);
+  const int split = (int)((tk / p.H) % p.num_splits);
+  const int b = (int)(tk / ((long long)p.H * p.num_splits));
+  const int kbeg = split * p.split_len, kend = min(p.N, kbeg + p.split_len);
+  const int qlen = p.split_len / P;  // a multiple of the tile size
+  const int wbeg = kbeg + part * qlen, wend = min(kend, wbeg + qlen);
+
+  const int r = lr;  // row (folded: token r/G, head r%G); p.M <= 32
+  const bool rvalid = r < p.M;
+  const int tok = rvalid ? r / p.G : 0, g = rvalid ? r - tok * p.G : 0;
+  int lim = -1;
+  if (rvalid && active) lim = max(min(p.qpos[(long long)b * p.qpBs + tok], wend - 1), -1);
+  if (lim < wbeg) lim = -1;
+  const int wmax = __builtin_amdgcn_readfirstlane(wave_max(lim));
+  const int wmin = __builtin_amdgcn_readfirstlane(wave_min(lim));
+  const int t_beg = wbeg / T::BN, t_end = wmax < wbeg ? t_beg : wmax / T::BN + 1;
+
+  const uint16_t* qrow = p.q + (long long)b * p.qsB + (long long)hk * p.qsH + (long long)tok * p.qsT + (long long)g * p.qsG;
+  bf16x8_t qf[T::QK];
+#pragma unroll
+  for (int ks = 0; ks < T::QK; ++ks)
+    qf[ks] = as_bf16x8(rvalid ? ld16(qrow + 16 * ks + 8 * hf) : u32x4_t{0u, 0u, 0u, 0u});
+  __builtin_amdgcn_s_waitcnt(vmcnt_le(0));  // Q has landed before the (untracked) tile loads start
+  const uint16_t* Kb = p.k + (long long)b * p.ksB + (long long)hk * p.ksH;
+  const uint16_t* Vb = p.v + (long long)b * p.vsB + (long long)hk * p.vsH;
+  const Dma<HD, 1> kplan(p.ksM, 0, lane), vplan(p.vsM, 0, lane);
+  const bool kfast = p.ksM * 2 * T::BN < (1ll << 31), vfast = p.vsM * 2 * T::BN < (1ll << 31);
+  const uint32_t kbase[2] = {k_lane_base<HD>(0, lr, hf), k_lane_base<HD>(1, lr, hf)};
+  const uint32_t vbase = v_lane_base<HD>(lane);
+  constexpr int DW = Dma<HD, 1>::DW;
+  uint8_t* kb = kbuf[w];
+  uint8_t* vb = vbuf[w];
+
+  f32x16_t o[T::DB];
+#pragma unroll
+  for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const float cc = p.scale_log2;
+  f32x16_t s[2];
+  uint32_t pk[2][8];
+
+  if (t_end > t_beg) {
+    kplan.template tile<true>(kb, Kb, p.ksM, kfast, t_beg * T::BN, wend, 0, lane);
+    vplan.template tile<true>(vb, Vb, p.vsM, vfast, t_beg * T::BN, wend, 0, lane);
+  }
+  for (int t = t_beg; t < t_end; ++t) {
+    const int k0 = t * T::BN;
+    const bool more = t + 1 < t_end;
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(DW));  // K(t) landed (V(t) may be in flight)
+    qk_tile<HD>(s, kb, qf, kbase);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the K tile has been read
+    if (more) kplan.template tile<true>(kb, Kb, p.ksM, kfast, k0 + T::BN, wend, 0, lane);
+    if (k0 + T::BN - 1 > wmin) {
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = k0 + 32 * kb2 + 8 * (v >> 2) + 4 * hf + (v & 3);
+          if (key > lim) s[kb2][v] = -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb2][v]);
+    mx = halves_max(mx) * cc;
+    if (__any(mx > m_run + RESCALE_SLACK)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float p0 = fast_exp2(__builtin_fmaf(s[kb2][2 * i], cc, -m_use));
+        const float p1 = fast_exp2(__builtin_fmaf(s[kb2][2 * i + 1], cc, -m_use));
+        ps[(i & 1) * 2] += p0;
+        ps[(i & 1) * 2 + 1] += p1;
+        pk[kb2][i] = pack_bf16x2(p0, p1);
+      }
+    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    if (more)
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(DW));  // V(t) landed, K(t+1) may be in flight
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+#pragma unroll
+    for (int ss = 0; ss < 4; ++ss) {
+      const u32x4_t pw = {pk[ss >> 1][4 * (ss & 1) + 0], pk[ss >> 1][4 * (ss & 1) + 1], pk[ss >> 1][4 * (ss & 1) + 2],
+                          pk[ss >> 1][4 * (ss & 1) + 3]};
+      const bf16x8_t pb = as_bf16x8(pw);
+#pragma unroll
+      for (int db = 0; db < T::DB; ++db) o[db] = mfma32(v_operand<HD>(vb, db, ss, vbase), pb, o[db]);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the V tile has been read
+    if (more) vplan.template tile<true>(vb, Vb, p.vsM, vfast, k0 + T::BN, wend, 0, lane);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+
+  // ---- merge the P partials of each split through LDS (the tile buffers are free once every wavefront is here)
+  const float l = halves_sum(l_run);
+  __syncthreads();
+  float* om = reinterpret_cast<float*>(&kbuf[0][0]);  // [DEC_NW][32 rows][HD]: wavefront w's slice is kbuf[w]
+  float* mm = reinterpret_cast<float*>(&vbuf[0][0]);  // [DEC_NW][32]
+  float* lm = mm + DEC_NW * 32;                       // [DEC_NW][32]
+#pragma unroll
+  for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d = 32 * db + 8 * q4 + 4 * hf;
+      *reinterpret_cast<f32x4_t*>(om + (w * 32 + lr) * HD + d) =
+          f32x4_t{o[db][4 * q4 + 0], o[db][4 * q4 + 1], o[db][4 * q4 + 2], o[db][4 * q4 + 3]};
+    }
+  if (hf == 0) {
+    mm[w * 32 + lr] = l > 0.f ? m_run : -INFINITY;
+    lm[w * 32 + lr] = l;
+  }
+  __syncthreads();
+  if (!active) return;
+  const int w0 = w - part;  // first wavefront of this split's group
+  const long long prow0 = ((long long)(b * p.H + hk) * p.num_splits + split) * p.M;
+  for (int idx = part * 64 + lane; idx < p.M * HD; idx += P * 64) {
+    const int row = idx / HD, d = idx - row * HD;
+    float mx = -INFINITY;
+    for (int ww = w0; ww < w0 + P; ++ww) mx = fmaxf(mx, mm[ww * 32 + row]);
+    float lsum = 0.f, acc = 0.f;
+    if (mx != -INFINITY) {
+      for (int ww = w0; ww < w0 + P; ++ww) {
+        const float mw = mm[ww * 32 + row];
+        const float f = mw == -INFINITY ? 0.f : fast_exp2(mw - mx);
+        lsum += f * lm[ww * 32 + row];
+        acc += f * om[(ww * 32 + row) * HD + d];
+      }
+    }
+    p.ws_o[(prow0 + row) * HD + d] = lsum > 0.f ? acc / lsum : 0.f;
+    if (d == 0) p.ws_lse[prow0 + row] = lsum > 0.f ? (mx + log2f(lsum)) * 0.69314718055994530942f : -INFINITY;
+  }
+}
+
 // LSE-weighted merge of the split partials: one wavefront per (b, kv head, row).
 //   lse = log(sum_s exp(lse_s)),  O = sum_s exp(lse_s - lse) * O_s     (O_s already normalised by its row sum)
+// Lane s holds split s's weight (64 splits per pass) and the partial rows are read in batches of 8 independent
+// loads per lane, so a row costs a few memory round trips rather than one per split.
+__device__ __forceinline__ float wave_maxf(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
+  return x;
+}
+__device__ __forceinline__ float wave_sumf(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
 template <int HD>
 __global__ void __launch_bounds__(256) splitkv_combine_kernel(const FwdParams p) {
   constexpr int DPL = HD / 64;  // dims per lane
+  constexpr int BATCH = 8;
   const long long wid = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (wid >= (long long)p.B * p.H * p.M) return;
@@ -713,23 +921,38 @@ __global__ void __launch_bounds__(256) splitkv_combine_kernel(const FwdParams p)
   const long long bh = wid / p.M;
   const int b = (int)(bh / p.H), hk = (int)(bh % p.H);
   const int S = p.num_splits;
-  const long long base = bh * S * p.M + r;
+  const long long base = bh * S * p.M + r;  // split s's partial row: base + s * M
   float mx = -INFINITY;
-  for (int s = 0; s < S; ++s) mx = fmaxf(mx, p.ws_lse[base + (long long)s * p.M]);
+  for (int s0 = 0; s0 < S; s0 += 64)
+    if (s0 + lane < S) mx = fmaxf(mx, p.ws_lse[base + (long long)(s0 + lane) * p.M]);
+  mx = wave_maxf(mx);
   float acc[DPL];
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+  for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
   float wsum = 0.f;
   if (mx != -INFINITY) {
-    for (int s = 0; s < S; ++s) {
-      const float wgt = fast_exp2((p.ws_lse[base + (long long)s * p.M] - mx) * 1.44269504088896340736f);
-      wsum += wgt;
-      if (wgt != 0.f) {
-        const float* po = p.ws_o + (base + (long long)s * p.M) * HD + DPL * lane;
+    for (int s0 = 0; s0 < S; s0 += 64) {
+      const int n = min(64, S - s0);
+      const float wl = lane < n ? fast_exp2((p.ws_lse[base + (long long)(s0 + lane) * p.M] - mx) * 1.44269504088896340736f)
+                                : 0.f;
+      wsum += wl;
+      for (int j0 = 0; j0 < n; j0 += BATCH) {
+        float v[BATCH][DPL], wj[BATCH];
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[j] += wgt * po[j];
+        for (int j = 0; j < BATCH; ++j) {
+          const int jj = min(j0 + j, n - 1);  // a clamped (in-bounds) row whose weight is zeroed below
+          const float* po = p.ws_o + (base + (long long)(s0 + jj) * p.M) * HD + DPL * lane;
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) v[j][e] = po[e];
+          wj[j] = j0 + j < n ? __shfl(wl, jj, 64) : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < BATCH; ++j)
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) acc[e] += wj[j] * v[j][e];
       }
     }
+    wsum = wave_sumf(wsum);
   }
   const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
   const int tok = r / p.G, g = r - tok * p.G;
@@ -833,9 +1056,25 @@ int launch_splitkv(const SplitParams& sp, int head_dim, hipStream_t stream) {
   const int per = (p.N + sp.num_splits - 1) / sp.num_splits;
   p.split_len = ((per + FwdTile<128>::BN - 1) / FwdTile<128>::BN) * FwdTile<128>::BN;
   if (p.split_len <= 0) p.split_len = FwdTile<128>::BN;
-  int rc = head_dim == 128 ? launch_fwd_t<128, MODE_QPOS, false, true>(p, stream)
-         : head_dim == 256 ? launch_fwd_t<256, MODE_QPOS, false, true>(p, stream)
-                           : (int)hipErrorInvalidValue;
+  int rc;
+  if (head_dim == 128 && p.M <= 32) {
+    // wavefront-split decode kernel: P wavefronts per split, each streaming at least DEC_MIN_TILES tiles when the
+    // split is long enough; split_len is a multiple of P tiles
+    constexpr int BN = FwdTile<128>::BN, DEC_MIN_TILES = 8;
+    const int q = (p.N + sp.num_splits - 1) / sp.num_splits;
+    const int qt = (q + BN - 1) / BN;
+    const int P = qt >= 4 * DEC_MIN_TILES ? 4 : qt >= 2 * DEC_MIN_TILES ? 2 : 1;
+    p.split_len = ((qt + P - 1) / P) * P * BN;
+    const long long ntask = (long long)p.B * p.H * p.num_splits;
+    const long long nwg = (ntask + (DEC_NW / P) - 1) / (DEC_NW / P);
+    if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
+    hipLaunchKernelGGL(fmha_decode_kernel<128>, dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
+    rc = (int)hipGetLastError();
+  } else {
+    rc = head_dim == 128 ? launch_fwd_t<128, MODE_QPOS, false, true>(p, stream)
+       : head_dim == 256 ? launch_fwd_t<256, MODE_QPOS, false, true>(p, stream)
+                         : (int)hipErrorInvalidValue;
+  }
   if (rc) return rc;
   const long long nrow = (long long)p.B * p.H * p.M;
   const long long nwg = (nrow + 3) / 4;

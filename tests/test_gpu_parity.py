@@ -289,7 +289,7 @@ def run_split(c, a, num_splits):
     return host(o), lse.cpu().numpy()
 
 
-@pytest.mark.parametrize("num_splits", [1, 3, 16, 40])
+@pytest.mark.parametrize("num_splits", [1, 3, 16, 40, 70])
 def test_splitkv_small(num_splits):
     rng = np.random.default_rng(80)
     B, N = 3, 1000
@@ -301,6 +301,18 @@ def test_splitkv_small(num_splits):
     o, lse = FC.oracle_ref(c, a)
     FC.check_tolerance(og, o, lg, lse, where=f"split{num_splits}")
     assert (og[2] == 0).all() and np.isneginf(lg[2]).all()
+
+
+@pytest.mark.parametrize("S,Hq,Hkv,N,splits", [(4, 32, 4, 2100, 7), (3, 8, 4, 70, 9), (1, 8, 8, 5000, 2),
+                                                (5, 32, 4, 1500, 4)])
+def test_splitkv_multitoken_d128(S, Hq, Hkv, N, splits):
+    # up to 32 folded rows per KV head take the wavefront-split decode kernel; (5, 32, 4) has 40 and does not
+    c = FC.Case(f"split_mt128_{S}_{Hq}_{Hkv}", B=2, S=S, N=N, Hq=Hq, Hkv=Hkv, D=128, mode="causal", seed=83)
+    _say(f"splitkv multi-token d128 S{S} Hq{Hq} Hkv{Hkv} N{N} splits{splits}")
+    a = FC.build(c)
+    og, lg = run_split(c, a, splits)
+    o, lse = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, o, lg, lse, where=c.name)
 
 
 def test_splitkv_multitoken_d256():
