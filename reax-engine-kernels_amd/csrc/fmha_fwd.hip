@@ -21,184 +21,13 @@
 //     first (v8:134-135) and, when B*H is a multiple of 8, each XCD's L2 serves a fixed set of KV heads.
 #include "fmha_common.h"
 #include "fmha_launch.h"
+#include "fmha_tiles.h"
 
 #include <climits>
 #include <type_traits>
 
 namespace reax {
 
-template <int HD>
-struct FwdTile {
-  static constexpr int BM = 128;       // folded query rows per workgroup (4 wavefronts x 32)
-  static constexpr int BN = 64;        // keys per K/V tile
-  static constexpr int NT = 256;       // threads per workgroup
-  static constexpr int KU = HD / 8;    // 16-byte units per K/V row
-  static constexpr int TILE = BN * HD * 2;  // bytes of one K or V tile
-  static constexpr int DMA = TILE / 1024;   // 64-lane x 16-byte direct-to-LDS loads per tile
-  static constexpr int DMA_W = DMA / 4;     // ... per wavefront
-  static constexpr int QK = HD / 16;        // MFMA k-steps of S^T = K Q^T
-  static constexpr int DB = HD / 32;        // 32-dim blocks of O^T
-  static_assert(HD == 128 || HD == 256, "head_dim 128 or 256");
-};
-
-// Row-major K/V tiles with a 16-byte-unit XOR swizzle for gfx950's 64-bank LDS (256 bytes per access phase):
-//   - K operand reads (ds_read_b128, 16 lanes per phase) touch 16 consecutive rows at one unit: f() is a
-//     bijection on r mod 16, so the 16 units land in 16 distinct bank groups;
-//   - transposed V reads (ds_read_b64_tr_b16, 32 lanes per phase) touch 4 consecutive rows x 4 adjacent units:
-//     bits 2-3 of f() (= r & 3) differ across the 4 rows, so the 16 (row, unit) pieces are distinct.
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-template <int HD>
-__device__ __forceinline__ uint32_t tile_off(int r, int u) {
-  return (uint32_t)(r * (HD * 2) + ((u ^ swz(r)) << 4));
-}
-
-__device__ __forceinline__ u32x4_t ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
-
-#define REAX_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-
-// One 16-byte direct global -> LDS load per lane (global_load_lds_dwordx4): lane l's bytes land at lds + 16 l.
-__device__ __forceinline__ void lds_dma16(const void* src, uint8_t* lds) {
-  __builtin_amdgcn_global_load_lds(src, REAX_LDS(lds), 16, 0, 0);
-}
-
-// The same load issued as inline assembly with the nontemporal hint, for data read exactly once (the K/V stream of
-// a decode step): measured on MI355X, a cold streaming read with nt runs at ~6.8 TB/s against ~3.9 TB/s without
-// it when the caches hold dirty lines. The compiler keeps no direct-to-LDS bookkeeping for inline assembly, so it
-// adds no conservative vmcnt(0) before later LDS reads of other buffers; the caller orders the load explicitly:
-// s_waitcnt vmcnt before reading the destination, lgkmcnt(0) after the last read of a region before loading into
-// it again.
-__device__ __forceinline__ void lds_dma16_stream(const void* src, uint8_t* lds) {
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(lds));
-  asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(src), "{m0}"(m0) : "memory");
-}
-
-// Direct global -> LDS copy of a K or V tile. Load c of a tile fills bytes [c*1024, c*1024 + 1024): lane l
-// lands at c*1024 + 16 l, i.e. row r, swizzled unit pu, and fetches the logical unit u = pu ^ swz(r) of that
-// row. With NWV wavefronts per workgroup, wavefront w issues loads c = w*DW .. w*DW + DW - 1 (DW = DMA / NWV).
-template <int HD, int NWV>
-struct Dma {
-  static constexpr int DW = FwdTile<HD>::DMA / NWV;
-  static_assert(DW >= 1 && DW * NWV == FwdTile<HD>::DMA, "tile loads split evenly over the wavefronts");
-  uint32_t off[DW];  // byte offset of this lane's source relative to the tile's first key row
-
-  __device__ __forceinline__ static void slot(int w, int i, int lane, int& r, int& u) {
-    const int byte = (w * DW + i) * 1024 + 16 * lane;
-    r = byte / (HD * 2);
-    u = ((byte % (HD * 2)) >> 4) ^ swz(r);
-  }
-  __device__ __forceinline__ Dma(long long stride, int w, int lane) {
-#pragma unroll
-    for (int i = 0; i < DW; ++i) {
-      int r, u;
-      slot(w, i, lane, r, u);
-      off[i] = (uint32_t)((long long)r * stride * 2 + 16 * u);
-    }
-  }
-  // Copies the tile at key k0. Full tiles (k0 + BN <= kend, and 32-bit row offsets) use the precomputed
-  // offsets; a partial last tile clamps its rows to the window's last key: those scores are masked, so they
-  // only ever meet a zero probability.
-  template <bool STREAM = false>
-  __device__ __forceinline__ void tile(uint8_t* buf, const uint16_t* base, long long stride, bool fast, int k0,
-                                       int kend, int w, int lane) const {
-    if (fast && k0 + FwdTile<HD>::BN <= kend) {
-      const uint16_t* tb = base + (long long)k0 * stride;
-#pragma unroll
-      for (int i = 0; i < DW; ++i) {
-        const uint8_t* src = reinterpret_cast<const uint8_t*>(tb) + off[i];
-        if (STREAM)
-          lds_dma16_stream(src, buf + (w * DW + i) * 1024);
-        else
-          lds_dma16(src, buf + (w * DW + i) * 1024);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < DW; ++i) {
-        int r, u;
-        slot(w, i, lane, r, u);
-        const int key = min(k0 + r, kend - 1);
-        if (STREAM)
-          lds_dma16_stream(base + (long long)key * stride + 8 * u, buf + (w * DW + i) * 1024);
-        else
-          lds_dma16(base + (long long)key * stride + 8 * u, buf + (w * DW + i) * 1024);
-      }
-    }
-  }
-};
-
-__device__ __forceinline__ void wait_dma_and_sync() {
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wavefront's direct-to-LDS loads have landed
-  __syncthreads();                     // ... and every other wavefront's
-}
-
-// LDS read addresses. Row offsets (multiples of HD*2) and the swizzled 16-byte unit (bits 4..8) occupy disjoint
-// bits, so every operand address is a per-lane base XOR a compile-time constant (plus a constant offset).
-//   K operand (kb, ks): row 32kb + lr, unit 2ks + hf  ->  kbase[kb] ^ (32 ks)
-//   V operand (db, ss, second half): row 16ss + 4h + i/4 + 8*second, unit 4db + 2dh + (i&3)/2, byte 8(i&1)
-//     -> (16ss + 8 second)*HD*2 + (vbase ^ vconst(db, second))
-template <int HD>
-__device__ __forceinline__ uint32_t k_lane_base(int kb, int lr, int hf) {
-  const int r = 32 * kb + lr;
-  return (uint32_t)(r * HD * 2 + ((hf ^ swz(r)) << 4));
-}
-// With row = 16ss + 4h + i/4 + 8 second, swz(row) = ((i/4) << 2) | h | (second << 1) and the unit is
-// 4db + 2dh + (i&3)/2, so unit ^ swz(row) = L(lane) ^ C(db, second) with the two parts below.
-template <int HD>
-__device__ __forceinline__ uint32_t v_lane_base(int lane) {
-  const int h = lane >> 5, dh = (lane >> 4) & 1, i = lane & 15;
-  const int L = (((i >> 1) & 1) ^ h) | (dh << 1) | (((i >> 2) & 3) << 2);
-  return (uint32_t)((4 * h + (i >> 2)) * HD * 2 + (L << 4) + 8 * (i & 1));
-}
-__device__ __forceinline__ constexpr uint32_t v_const(int db, int second) {
-  return (uint32_t)(((second << 1) | ((db & 3) << 2) | (((db >> 2) & 1) << 4)) << 4);
-}
-
-// S^T for one 64-key tile: s[kb][v] = score of this lane's row against key 32kb + 8(v/4) + 4hf + v%4.
-template <int HD>
-__device__ __forceinline__ void qk_tile(f32x16_t (&s)[2], const uint8_t* kbuf, const bf16x8_t (&qf)[HD / 16],
-                                        const uint32_t (&kbase)[2]) {
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-    for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < HD / 16; ++ks) {
-      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kbuf + (kbase[kb] ^ (32u * ks)));
-      s[kb] = mfma32(as_bf16x8(kf), qf[ks], s[kb]);
-    }
-  }
-}
-
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ u32x2_t ds_read_tr16(const uint8_t* p) {
-  const i16x4_t a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) i16x4_t*)(p));
-  return __builtin_bit_cast(u32x2_t, a);
-}
-
-// V^T operand (32 dims x 16 keys in MFMA key order) of dim block db, k-step ss, from the row-major V tile with
-// two ds_read_b64_tr_b16: in each 16-lane group, lane i reads 4 dims of key row i/4 and receives 4 keys of
-// dim i back.
-template <int HD>
-__device__ __forceinline__ bf16x8_t v_operand(const uint8_t* vbuf, int db, int ss, uint32_t vbase) {
-  const u32x2_t a = ds_read_tr16(vbuf + 16 * ss * HD * 2 + (vbase ^ v_const(db, 0)));
-  const u32x2_t b = ds_read_tr16(vbuf + (16 * ss + 8) * HD * 2 + (vbase ^ v_const(db, 1)));
-  return as_bf16x8(u32x4_t{a[0], a[1], b[0], b[1]});
-}
-
-__device__ __forceinline__ int wave_max(int x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x = max(x, __shfl_xor(x, off, 64));
-  return x;
-}
-__device__ __forceinline__ int wave_min(int x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x = min(x, __shfl_xor(x, off, 64));
-  return x;
-}
-
-// Lazy rescaling: the running max (log2 units) is raised only when a tile's max exceeds it by more than
-// RESCALE_SLACK, so probabilities stay below 2^RESCALE_SLACK and the O / row-sum rescale is rare.
-constexpr float RESCALE_SLACK = 8.0f;
 
 template <int HD, int MODE, bool POST, bool SPLIT>
 __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const FwdParams p, int o_vec8) {
@@ -486,6 +315,9 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
 //     half 2 of step t: the roles swap.
 // While one wavefront of a SIMD keeps the matrix core busy, the other one does its exponentials, so the
 // MFMA pipe never waits for a softmax. K(t+1) and V(t) stream into LDS during step t (two buffers each).
+#ifndef REAX_FWD_FA
+#define REAX_FWD_FA 0
+#endif
 constexpr int PP_NW = 8;
 #ifndef REAX_PP_STAGES
 #define REAX_PP_STAGES 2
@@ -655,20 +487,20 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
     constexpr int PER_STEP = 2 * Dma<HD, PP_NW>::DW;  // loads per wavefront per step
 #pragma unroll
     for (int j = 0; j < NS - 1; ++j)
-      if (j < t_end) kplan.tile(kring[j], Kb, p.ksM, kfast, j * T::BN, Nb, w, lane);
+      if (j < t_end) kplan.template tile<1>(kring[j], Kb, p.ksM, kfast, j * T::BN, Nb, w, lane);
 #pragma unroll
     for (int j = 0; j < NS - 2; ++j)
-      if (j < t_end) vplan.tile(vring[j], Vb, p.vsM, vfast, j * T::BN, Nb, w, lane);
+      if (j < t_end) vplan.template tile<1>(vring[j], Vb, p.vsM, vfast, j * T::BN, Nb, w, lane);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // all prologue loads (simplest: the first step needs K(0) anyway)
     __syncthreads();
     auto step = [&](int t, const uint8_t* kb_t, uint8_t* kb_fill, const uint8_t* vb_prev, uint8_t* vb_fill) __attribute__((always_inline)) {
-      if (t + NS - 1 < t_end) kplan.tile(kb_fill, Kb, p.ksM, kfast, (t + NS - 1) * T::BN, Nb, w, lane);
-      if (t + NS - 2 < t_end) vplan.tile(vb_fill, Vb, p.vsM, vfast, (t + NS - 2) * T::BN, Nb, w, lane);
+      if (t + NS - 1 < t_end) kplan.template tile<1>(kb_fill, Kb, p.ksM, kfast, (t + NS - 1) * T::BN, Nb, w, lane);
+      if (t + NS - 2 < t_end) vplan.template tile<1>(vb_fill, Vb, p.vsM, vfast, (t + NS - 2) * T::BN, Nb, w, lane);
       if (grp == 0)
         mfma_phase(t, kb_t, vb_prev);
       else if (t >= 1)
         softmax(t - 1);
-      __syncthreads();
+      exec_barrier();  // staggers the two groups; no data passes here, so the loads issued above stay in flight
       if (grp == 0) {
         if (t < t_end) softmax(t);
       } else {
@@ -790,8 +622,8 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   uint32_t pk[2][8];
 
   if (t_end > t_beg) {
-    kplan.template tile<true>(kb, Kb, p.ksM, kfast, t_beg * T::BN, wend, 0, lane);
-    vplan.template tile<true>(vb, Vb, p.vsM, vfast, t_beg * T::BN, wend, 0, lane);
+    kplan.template tile<2>(kb, Kb, p.ksM, kfast, t_beg * T::BN, wend, 0, lane);
+    vplan.template tile<2>(vb, Vb, p.vsM, vfast, t_beg * T::BN, wend, 0, lane);
   }
   for (int t = t_beg; t < t_end; ++t) {
     const int k0 = t * T::BN;
@@ -799,7 +631,7 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
     __builtin_amdgcn_s_waitcnt(vmcnt_le(DW));  // K(t) landed (V(t) may be in flight)
     qk_tile<HD>(s, kb, qf, kbase);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the K tile has been read
-    if (more) kplan.template tile<true>(kb, Kb, p.ksM, kfast, k0 + T::BN, wend, 0, lane);
+    if (more) kplan.template tile<2>(kb, Kb, p.ksM, kfast, k0 + T::BN, wend, 0, lane);
     if (k0 + T::BN - 1 > wmin) {
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2)
@@ -851,7 +683,7 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
       for (int db = 0; db < T::DB; ++db) o[db] = mfma32(v_operand<HD>(vb, db, ss, vbase), pb, o[db]);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the V tile has been read
-    if (more) vplan.template tile<true>(vb, Vb, p.vsM, vfast, k0 + T::BN, wend, 0, lane);
+    if (more) vplan.template tile<2>(vb, Vb, p.vsM, vfast, k0 + T::BN, wend, 0, lane);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
 
@@ -1017,8 +849,15 @@ int launch_fwd(const FwdParams& p0, int head_dim, int mode, bool post, hipStream
   // head_dim 128 qpos / varlen without the POST epilogue: the ping-pong kernel once a row tile has enough rows
   // to fill both groups (short query blocks, e.g. decode, keep the 4-wavefront kernel)
   if (head_dim == 128 && !post && p.M > FwdTile<128>::BM) {
+#if REAX_FWD_FA
+    if (mode == MODE_QPOS || mode == MODE_VARLEN) {
+      const int o_vec8 = p.o ? (aligned_elems(p.o, 4, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0) : 0;
+      return launch_fwd_fa(p, mode, o_vec8, stream);
+    }
+#else
     if (mode == MODE_QPOS) return launch_fwd_pp<MODE_QPOS>(p, stream);
     if (mode == MODE_VARLEN) return launch_fwd_pp<MODE_VARLEN>(p, stream);
+#endif
   }
   if (head_dim == 128) {
     if (mode == MODE_QPOS)
