@@ -85,15 +85,6 @@ __device__ __forceinline__ void scale_acc(f32x16_t& acc, float s) {
     acc[e] = x;
   }
 }
-// f(std::integral_constant<int, I>) for I = B .. E-1, expanded at compile time (a 32-step "#pragma unroll" loop
-// over the interleaved block exceeds the unroller's size limit and would stay a loop with dynamic indexing)
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
 // Redefines x in place (no instruction). Volatile statements keep their order, so touching a chunk's inputs right
 // after its MFMA and its outputs before the next one confines the chunk's VALU work to that slot; scheduling
 // barriers alone do not, as instruction selection already sinks side-effect-free arithmetic towards its uses.

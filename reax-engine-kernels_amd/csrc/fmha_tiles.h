@@ -80,6 +80,29 @@ struct Dma {
       off[i] = (uint32_t)((long long)r * stride * 2 + 16 * u);
     }
   }
+  // One of the DW loads of tile(): load i only, so that a caller can spread a tile's loads over time.
+  template <int KIND = 0>
+  __device__ __forceinline__ void load_one(int i, uint8_t* buf, const uint16_t* base, long long stride, bool fast,
+                                           int k0, int kend, int w, int lane) const {
+    // The per-lane inputs pass through empty asm so that the compiler derives the addresses here, where the
+    // load is issued, instead of keeping them live (or spilled) from the kernel's start.
+    const uint8_t* src;
+    if (fast && k0 + BN <= kend) {
+      uint32_t o = off[i];
+      asm volatile("" : "+v"(o));
+      src = reinterpret_cast<const uint8_t*>(base + (long long)k0 * stride) + o;
+    } else {
+      int r, u, ln = lane;
+      asm volatile("" : "+v"(ln));
+      slot(w, i, ln, r, u);
+      const int key = min(k0 + r, kend - 1);
+      src = reinterpret_cast<const uint8_t*>(base + (long long)key * stride + 8 * u);
+    }
+    if (KIND)
+      lds_dma16_asm<KIND == 2>(src, buf + (w * DW + i) * 1024);
+    else
+      lds_dma16(src, buf + (w * DW + i) * 1024);
+  }
   // Copies the tile at key k0. Full tiles (k0 + BN <= kend, and 32-bit row offsets) use the precomputed
   // offsets; a partial last tile clamps its rows to the window's last key: those scores are masked, so they
   // only ever meet a zero probability.
@@ -111,6 +134,16 @@ struct Dma {
     }
   }
 };
+
+// f(std::integral_constant<int, I>) for I = B .. E-1, expanded at compile time (a 32-step "#pragma unroll" loop
+// over a long interleaved block exceeds the unroller's size limit and would stay a loop with dynamic indexing)
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 // Workgroup barrier that orders execution only. __syncthreads() also fences memory, which makes every wavefront
 // wait at the barrier for its in-flight direct-to-LDS loads (vmcnt(0)); the memory clobber keeps the compiler
