@@ -101,6 +101,27 @@ __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
 // ulp, plus a few ulp for v_exp_f32, the add and v_rcp_f32. Whenever the fp32 result lies within 256 ulp of a
 // bf16 rounding midpoint, or |x| >= 64, the value is recomputed in double precision, whose error is far below
 // the distance to any midpoint; otherwise rounding the fp32 value to bf16 gives the correctly rounded result.
+// Correctly rounded bf16 sigmoid of a gate whose fp32 fast path may round the wrong way (near a bf16 midpoint)
+// or lose accuracy (|x| >= 64): double precision. Kept out of line: the epilogue calls it for a few gates at most,
+// and inlined at each of its call sites the double-precision code would raise the register count of the whole
+// kernel, main loop included.
+__device__ __attribute__((noinline)) uint32_t sigmoid_bf16_slow(float x) {
+  if (x != x) return 0x7fc0u;
+  const double xd = (double)x;
+  const double sd = xd >= 0.0 ? 1.0 / (1.0 + exp(-xd)) : exp(xd) / (1.0 + exp(xd));
+  // sd is in [0, 1]: round it to the bf16 grid of its binade (8 significant bits, or the subnormal
+  // spacing 2^-133 below 2^-126) with round-half-even.
+  if (sd == 0.0) return 0u;
+  int ex;
+  const double m = frexp(sd, &ex);  // sd = m * 2^ex, m in [0.5, 1)
+  double r;
+  if (ex - 1 < -126) {
+    r = ldexp(rint(ldexp(sd, 133)), -133);  // bf16 subnormal spacing 2^-133
+  } else {
+    r = ldexp(rint(ldexp(m, 8)), ex - 8);
+  }
+  return __float_as_uint((float)r) >> 16;
+}
 __device__ __forceinline__ uint32_t sigmoid_bf16_bits(uint32_t gbits) {
   const float x = __uint_as_float(gbits << 16);
   const float e = fast_exp2(x * -1.44269504088896340736f);
@@ -109,23 +130,7 @@ __device__ __forceinline__ uint32_t sigmoid_bf16_bits(uint32_t gbits) {
   const uint32_t low = u & 0xffffu;
   const bool near_tie = (low > 0x8000u - 256u) && (low < 0x8000u + 256u);
   const bool bad = near_tie || !(x > -64.0f && x < 64.0f);
-  if (__builtin_expect(bad, 0)) {
-    if (x != x) return 0x7fc0u;
-    const double xd = (double)x;
-    const double sd = xd >= 0.0 ? 1.0 / (1.0 + exp(-xd)) : exp(xd) / (1.0 + exp(xd));
-    // sd is in [0, 1]: round it to the bf16 grid of its binade (8 significant bits, or the subnormal
-    // spacing 2^-133 below 2^-126) with round-half-even.
-    if (sd == 0.0) return 0u;
-    int ex;
-    const double m = frexp(sd, &ex);  // sd = m * 2^ex, m in [0.5, 1)
-    double r;
-    if (ex - 1 < -126) {
-      r = ldexp(rint(ldexp(sd, 133)), -133);  // bf16 subnormal spacing 2^-133
-    } else {
-      r = ldexp(rint(ldexp(m, 8)), ex - 8);
-    }
-    return __float_as_uint((float)r) >> 16;
-  }
+  if (__builtin_expect(bad, 0)) return sigmoid_bf16_slow(x);
   return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 

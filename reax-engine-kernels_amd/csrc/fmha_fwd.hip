@@ -314,7 +314,10 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
 //                       group 1 runs its VALU phase  [softmax of S(t-1) -> P(t-1)]
 //     half 2 of step t: the roles swap.
 // While one wavefront of a SIMD keeps the matrix core busy, the other one does its exponentials, so the
-// MFMA pipe never waits for a softmax. K(t+1) and V(t) stream into LDS during step t (two buffers each).
+// MFMA pipe never waits for a softmax. K(t+1) and V(t) stream into LDS during step t (two buffers each): group 0
+// issues all of a step's loads, one after every fourth MFMA of its MFMA phase (measured: the 32 direct-to-LDS
+// loads of a step issued by all wavefronts at the start of the step held each of them up for ~480 clocks; spread
+// this way they cost group 0 ~45 clocks each, while its matrix core work continues).
 #ifndef REAX_FWD_FA
 #define REAX_FWD_FA 0
 #endif
@@ -334,6 +337,7 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   __shared__ int s_lim[PP_NW];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hf = lane >> 5, lr = lane & 31;
   const int grp = w >> 2;
+  const uint32_t wu = __builtin_amdgcn_readfirstlane(w);  // the wavefront index as a scalar, for load addresses
 
   // ---- workgroup -> (batch, KV head, row tile): heaviest tile first; XCD-aware when B*H % 8 == 0
   const int BH = p.B * p.H, id = blockIdx.x;
@@ -394,7 +398,7 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   f32x16_t s[2];
   uint32_t pk[2][8];
 
-  const Dma<HD, PP_NW> kplan(p.ksM, w, lane), vplan(p.vsM, w, lane);
+  const Dma<HD, PP_NW / 2> kplan(p.ksM, w, lane), vplan(p.vsM, w, lane);  // used by group 0 only
   const bool kfast = p.ksM * 2 * T::BN < (1ll << 31), vfast = p.vsM * 2 * T::BN < (1ll << 31);
   const uint32_t kbase[2] = {k_lane_base<HD>(0, lr, hf), k_lane_base<HD>(1, lr, hf)};
   const uint32_t vbase = v_lane_base<HD>(lane);
@@ -442,69 +446,124 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
       }
     l_run += psum;
   };
-  // MFMA phase of step t: O += V(t-1)^T P(t-1)^T, then S(t) = K(t) Q^T. When both halves run (the common
-  // case) they form one straight-line block whose order is pinned: LDS operand reads run four MFMAs ahead of
-  // their use, so the matrix core never waits for LDS.
-  auto pv_part = [&](const uint8_t* vb_prev) __attribute__((always_inline)) {
+  // MFMA phase of step t: O += V(t-1)^T P(t-1)^T (if PV), then S(t) = K(t) Q^T (if QK), one slot per MFMA in a
+  // fixed order (scheduling barriers between slots): each LDS operand read goes out D = 4 MFMAs ahead of its
+  // use, and dma(j), j = 0..7, one of the step's tile loads, after every (NOPS / 8)-th MFMA.
+  auto mfma_block = [&](auto pvc, auto qkc, const uint8_t* kb_t, const uint8_t* vb_prev,
+                        auto&& dma) __attribute__((always_inline)) {
+    constexpr bool PV = decltype(pvc)::value, QK = decltype(qkc)::value;
+    constexpr int NP = PV ? 16 : 0, NOPS = NP + (QK ? 16 : 0), D = 4;
+    bf16x8_t opr[D];
+    // operand i: i < NP: V^T (k-step ss = i/4, dim block db = i%4); then K (kb = j%2, ks = j/2), j = i - NP
+    auto read = [&](auto ic) __attribute__((always_inline)) {
+      constexpr int i = decltype(ic)::value;
+      if constexpr (i < NP) {
+        opr[i % D] = v_operand<HD>(vb_prev, i & 3, i >> 2, vbase);
+      } else {
+        constexpr int j = i - NP;
+        opr[i % D] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(kb_t + (kbase[j & 1] ^ (32u * (j >> 1)))));
+      }
+    };
+    if constexpr (NOPS == 0) {
+      static_for<0, 8>([&](auto jc) __attribute__((always_inline)) { dma(decltype(jc)::value); });
+    } else {
+      static_for<0, D>([&](auto ic) __attribute__((always_inline)) { read(ic); });
+      if constexpr (QK) {
 #pragma unroll
-    for (int ss = 0; ss < 4; ++ss) {
-      const u32x4_t pw = {pk[ss >> 1][4 * (ss & 1) + 0], pk[ss >> 1][4 * (ss & 1) + 1],
-                          pk[ss >> 1][4 * (ss & 1) + 2], pk[ss >> 1][4 * (ss & 1) + 3]};
-      const bf16x8_t pb = as_bf16x8(pw);
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int db = 0; db < T::DB; ++db) o[db] = mfma32(v_operand<HD>(vb_prev, db, ss, vbase), pb, o[db]);
+          for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<0, NOPS>([&](auto ic) __attribute__((always_inline)) {
+        constexpr int i = decltype(ic)::value;
+        if constexpr (i < NP) {
+          constexpr int ss = i >> 2, db = i & 3;
+          const u32x4_t pw = {pk[ss >> 1][4 * (ss & 1) + 0], pk[ss >> 1][4 * (ss & 1) + 1],
+                              pk[ss >> 1][4 * (ss & 1) + 2], pk[ss >> 1][4 * (ss & 1) + 3]};
+          o[db] = mfma32(opr[i % D], as_bf16x8(pw), o[db]);
+        } else {
+          constexpr int j = i - NP, kb = j & 1, ks = j >> 1;
+          s[kb] = mfma32(opr[i % D], qf[ks], s[kb]);
+        }
+        if constexpr (i + D < NOPS) read(std::integral_constant<int, i + D>{});
+        constexpr int GAP = NOPS / 8;
+        if constexpr (i % GAP == GAP / 2) dma(i / GAP);
+        __builtin_amdgcn_sched_barrier(0);
+      });
     }
   };
-  auto mfma_phase = [&](int t, const uint8_t* kb_t, const uint8_t* vb_prev) __attribute__((always_inline)) {
+  auto mfma_phase = [&](int t, const uint8_t* kb_t, const uint8_t* vb_prev, auto&& dma) __attribute__((always_inline)) {
     const bool pv = t >= 1 && (t - 1) * T::BN <= wmax;
     const bool qk = t < t_end && t * T::BN <= wmax;
-    if (pv && qk) {
-      pv_part(vb_prev);
-      qk_tile<HD>(s, kb_t, qf, kbase);
-      // pinned order: 8 V reads, then 16 x [PV MFMA, 2 reads], then 16 x [QK MFMA, 1 read]
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-    } else if (pv) {
-      pv_part(vb_prev);
-    } else if (qk) {
-      qk_tile<HD>(s, kb_t, qf, kbase);
-    }
+    using Y = std::true_type;
+    using N = std::false_type;
+    if (pv && qk)
+      mfma_block(Y{}, Y{}, kb_t, vb_prev, dma);
+    else if (pv)
+      mfma_block(Y{}, N{}, kb_t, vb_prev, dma);
+    else if (qk)
+      mfma_block(N{}, Y{}, kb_t, vb_prev, dma);
+    else
+      mfma_block(N{}, N{}, kb_t, vb_prev, dma);
   };
 
   if (t_end > 0) {
     // ring of NS stages: step t reads K(t) from kring[t % NS] and V(t-1) from vring[(t-1) % NS]; it fills
     // kring[(t-1) % NS] with K(t+NS-1) and vring[(t-2) % NS] with V(t+NS-2), whose previous contents were
-    // last read in step t-1. Each step waits only for the loads issued NS-2 steps earlier.
-    constexpr int PER_STEP = 2 * Dma<HD, PP_NW>::DW;  // loads per wavefront per step
+    // last read in step t-1. Each step waits only for the loads issued NS-2 steps earlier. Group 0 issues
+    // every load (DW = 4 per tile and wavefront); group 1 none.
+    constexpr int PER_STEP = 2 * Dma<HD, PP_NW / 2>::DW;  // loads per group-0 wavefront per step
+    static_assert(Dma<HD, PP_NW / 2>::DW == 4, "dma(j): j = 0..3 the K tile's loads, 4..7 the V tile's");
+    if (grp == 0) {
 #pragma unroll
-    for (int j = 0; j < NS - 1; ++j)
-      if (j < t_end) kplan.template tile<1>(kring[j], Kb, p.ksM, kfast, j * T::BN, Nb, w, lane);
+      for (int j = 0; j < NS - 1; ++j)
+        if (j < t_end) kplan.template tile<1>(kring[j], Kb, p.ksM, kfast, j * T::BN, Nb, w, lane);
 #pragma unroll
-    for (int j = 0; j < NS - 2; ++j)
-      if (j < t_end) vplan.template tile<1>(vring[j], Vb, p.vsM, vfast, j * T::BN, Nb, w, lane);
+      for (int j = 0; j < NS - 2; ++j)
+        if (j < t_end) vplan.template tile<1>(vring[j], Vb, p.vsM, vfast, j * T::BN, Nb, w, lane);
+    }
     __builtin_amdgcn_s_waitcnt(0x0F70);  // all prologue loads (simplest: the first step needs K(0) anyway)
     __syncthreads();
     auto step = [&](int t, const uint8_t* kb_t, uint8_t* kb_fill, const uint8_t* vb_prev, uint8_t* vb_fill) __attribute__((always_inline)) {
-      if (t + NS - 1 < t_end) kplan.template tile<1>(kb_fill, Kb, p.ksM, kfast, (t + NS - 1) * T::BN, Nb, w, lane);
-      if (t + NS - 2 < t_end) vplan.template tile<1>(vb_fill, Vb, p.vsM, vfast, (t + NS - 2) * T::BN, Nb, w, lane);
-      if (grp == 0)
-        mfma_phase(t, kb_t, vb_prev);
+      // Group 0's loads of this step: K(t+NS-1) and V(t+NS-2). When both are whole tiles with 32-bit row offsets
+      // (every step but the last one or two), each load is a per-lane offset added to a scalar tile base, issued
+      // from inside the MFMA block without a branch; otherwise they go out before the block.
+      const bool kload = t + NS - 1 < t_end, vload = t + NS - 2 < t_end;
+      const int kk0 = (t + NS - 1) * T::BN, vk0 = (t + NS - 2) * T::BN;
+      const bool inblock = kload && vload && kfast && vfast && kk0 + T::BN <= Nb && vk0 + T::BN <= Nb;
+      const uint8_t* ksrc = reinterpret_cast<const uint8_t*>(Kb + (long long)kk0 * p.ksM);
+      const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(Vb + (long long)vk0 * p.vsM);
+      constexpr int DW4 = Dma<HD, PP_NW / 2>::DW;
+      auto dma = [&](int j) __attribute__((always_inline)) {
+        const bool isk = j < DW4;
+        const int i = isk ? j : j - DW4;
+        // the offset passes through empty asm so that its 64-bit form is not kept live across the loop
+        uint32_t o = isk ? kplan.off[i] : vplan.off[i];
+        asm volatile("" : "+v"(o));
+        const uint8_t* src = (isk ? ksrc : vsrc) + o;
+        const uint32_t m0 = (uint32_t)reinterpret_cast<uintptr_t>(isk ? kb_fill : vb_fill) + (wu * DW4 + i) * 1024;
+        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+      };
+      auto no_dma = [](int) {};
+      if (grp == 0 && !inblock) {
+#pragma unroll
+        for (int i = 0; i < DW4; ++i) {
+          if (kload) kplan.template load_one<1>(i, kb_fill, Kb, p.ksM, kfast, kk0, Nb, w, lane);
+          if (vload) vplan.template load_one<1>(i, vb_fill, Vb, p.vsM, vfast, vk0, Nb, w, lane);
+        }
+      }
+      if (grp == 0 && inblock)
+        mfma_phase(t, kb_t, vb_prev, dma);
+      else if (grp == 0)
+        mfma_phase(t, kb_t, vb_prev, no_dma);
       else if (t >= 1)
         softmax(t - 1);
       exec_barrier();  // staggers the two groups; no data passes here, so the loads issued above stay in flight
       if (grp == 0) {
         if (t < t_end) softmax(t);
       } else {
-        mfma_phase(t, kb_t, vb_prev);
+        mfma_phase(t, kb_t, vb_prev, no_dma);
       }
       // K(t+1) and V(t) must have landed: they were issued NS-2 steps ago (or in the prologue), and loads return
       // in issue order, so vmcnt((NS-2) * PER_STEP) leaves exactly the loads of the last NS-2 steps in flight.
