@@ -339,10 +339,18 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   const int grp = w >> 2;
   const uint32_t wu = __builtin_amdgcn_readfirstlane(w);  // the wavefront index as a scalar, for load addresses
 
-  // ---- workgroup -> (batch, KV head, row tile): heaviest tile first; XCD-aware when B*H % 8 == 0
-  const int BH = p.B * p.H, id = blockIdx.x;
+  // ---- persistent workgroups: the grid has at most one workgroup per CU, and each works through items (row
+  // tiles of one (batch, KV head)) in a fixed order. Item ids follow the work order, heaviest tile first; when
+  // B*H % 8 == 0 the 8 XCDs (workgroups are dealt to them round-robin) each own the KV heads bh = x mod 8, so
+  // a head's K/V stays in one XCD's L2. Within its class, workgroup m takes items m, 2P'-1-m, 2P'+m, ... (P'
+  // workgroups in the class): a heavy item and a light one in turn, so the per-workgroup work evens out without
+  // relying on the order in which the hardware hands workgroups to CUs.
+  const int BH = p.B * p.H;
+  const long long n_items = (long long)BH * p.n_tiles;
+  const bool xcd_aware = (BH & 7) == 0 && (gridDim.x & 7) == 0;
+  auto item = [&](int id) __attribute__((always_inline)) {
   int bh, rank;
-  if ((BH & 7) == 0) {
+  if (xcd_aware) {
     const int per = BH >> 3, x = id & 7, j = id >> 3;
     bh = x + 8 * (j % per);
     rank = j / per;
@@ -610,6 +618,24 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
         *reinterpret_cast<uint32_t*>(orow + d + 2) = w1;
       }
     }
+  };  // item
+
+  const int P = gridDim.x;
+  for (int it = 0;; ++it) {
+    long long vid;
+    if (xcd_aware) {
+      const int x = blockIdx.x & 7, m = blockIdx.x >> 3, PX = P >> 3;
+      vid = 8ll * ((long long)it * PX + ((it & 1) ? PX - 1 - m : m)) + x;
+    } else {
+      vid = (long long)it * P + ((it & 1) ? P - 1 - (int)blockIdx.x : (int)blockIdx.x);
+    }
+    if (vid >= n_items) break;
+    // every wavefront is done with the previous item's s_lim and K/V buffers (its last LDS read was followed by a
+    // full barrier). Not __syncthreads(): its fence would wait for the previous item's output stores, whose
+    // latency instead overlaps the next item's first loads.
+    exec_barrier();
+    item((int)vid);
+  }
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -892,11 +918,27 @@ static int prepare(FwdParams& p, bool post) {
   return 0;
 }
 
+// Compute units of the current device (cached per device): the persistent kernels launch one workgroup per CU.
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <int MODE>
 static int launch_fwd_pp(FwdParams p, hipStream_t stream) {
   p.n_tiles = (int)(((long long)p.M + PP_BM - 1) / PP_BM);
-  const long long nwg = (long long)p.B * p.H * p.n_tiles;
-  if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  const long long n_items = (long long)p.B * p.H * p.n_tiles;
+  if (n_items <= 0 || n_items > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  const int cus = device_cus();
+  if (cus <= 0) return (int)hipErrorInvalidDevice;
+  const long long nwg = n_items < cus ? n_items : cus;  // one workgroup per CU (its LDS and registers fill one)
   const int o_vec8 = p.o ? (aligned_elems(p.o, 4, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0) : 0;
   hipLaunchKernelGGL((fmha_fwd_pp_kernel<MODE, REAX_PP_STAGES>), dim3((unsigned)nwg), dim3(64 * PP_NW), 0, stream, p, o_vec8);
   return (int)hipGetLastError();
