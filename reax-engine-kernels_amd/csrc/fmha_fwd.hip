@@ -342,12 +342,13 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   // ---- persistent workgroups: the grid has at most one workgroup per CU, and each works through items (row
   // tiles of one (batch, KV head)) in a fixed order. Item ids follow the work order, heaviest tile first; when
   // B*H % 8 == 0 the 8 XCDs (workgroups are dealt to them round-robin) each own the KV heads bh = x mod 8, so
-  // a head's K/V stays in one XCD's L2. Within its class, workgroup m takes items m, 2P'-1-m, 2P'+m, ... (P'
+  // a head's K/V stays in one XCD's L2 (not for varlen, whose sequences differ in length: there a fixed
+  // head-to-XCD split leaves some XCDs with more work than others). Within its class, workgroup m takes items m, 2P'-1-m, 2P'+m, ... (P'
   // workgroups in the class): a heavy item and a light one in turn, so the per-workgroup work evens out without
   // relying on the order in which the hardware hands workgroups to CUs.
   const int BH = p.B * p.H;
   const long long n_items = (long long)BH * p.n_tiles;
-  const bool xcd_aware = (BH & 7) == 0 && (gridDim.x & 7) == 0;
+  const bool xcd_aware = MODE != MODE_VARLEN && (BH & 7) == 0 && (gridDim.x & 7) == 0;
   auto item = [&](int id) __attribute__((always_inline)) {
   int bh, rank;
   if (xcd_aware) {
