@@ -442,18 +442,30 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
       m_run = m_new;
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    float psum = 0.f;
+    // three passes over the 32 elements (arguments, exponentials, sums and packing) with scheduling barriers in
+    // between: every instruction of a pass is independent of the others, so one wavefront issues them back to
+    // back instead of waiting on each exponential's input and result in turn
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) s[kb][v] = __builtin_fmaf(s[kb][v], cc, -m_use);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) s[kb][v] = fast_exp2(s[kb][v]);
+    __builtin_amdgcn_sched_barrier(0);
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float p0 = fast_exp2(__builtin_fmaf(s[kb][2 * i], cc, -m_use));
-        const float p1 = fast_exp2(__builtin_fmaf(s[kb][2 * i + 1], cc, -m_use));
-        psum += p0;
-        psum += p1;
-        pk[kb][i] = pack_bf16x2(p0, p1);
+        ps[(i & 1) * 2] += s[kb][2 * i];
+        ps[(i & 1) * 2 + 1] += s[kb][2 * i + 1];
+        pk[kb][i] = pack_bf16x2(s[kb][2 * i], s[kb][2 * i + 1]);
       }
-    l_run += psum;
+    l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
   };
   // MFMA phase of step t: O += V(t-1)^T P(t-1)^T (if PV), then S(t) = K(t) Q^T (if QK), one slot per MFMA in a
   // fixed order (scheduling barriers between slots): each LDS operand read goes out D = 4 MFMAs ahead of its
