@@ -107,6 +107,20 @@ def test_qx_qpos_edges():
             assert (og[0, m, hq] == a["v"][0, 0, hq // c.G]).all(), "qpos = 0 must write V[0] exactly"
 
 
+# The head_dim-128 prefill kernel is persistent (one workgroup per CU, items in snake order, an XCD-aware split
+# when B*H % 8 == 0): these shapes give more items than CUs, so workgroups run several items, in both orders.
+@pytest.mark.parametrize("B,S,Hq,Hkv", [(2, 2304, 16, 8), (1, 11264, 6, 3)], ids=["xcd_split", "plain_order"])
+def test_qx_persistent_multi_item(B, S, Hq, Hkv):
+    c = FC.Case(f"persist_b{B}_s{S}", B=B, S=S, N=S, Hq=Hq, Hkv=Hkv, D=128, mode="causal", seed=23 + B)
+    _say(f"qx persistent B{B} S{S} Hq{Hq} Hkv{Hkv} ({B * Hkv * -(-S * (Hq // Hkv) // 256)} items)")
+    a = FC.build(c)
+    og, lg = run_qx(c, a)
+    toks = token_subset(S, 48, 31 + B, edge=32)
+    o, lse = oracle_on_tokens(c, a, toks)
+    FC.check_tolerance(og[:, toks], o, lg[:, :, toks], lse, where=c.name)
+    assert np.isfinite(W.bf16_bits_to_f32(og)).all()
+
+
 GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
 
 
