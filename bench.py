@@ -141,8 +141,11 @@ def cpu_baseline(target_s=10.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # The MI355X raises its clock over the first ~30 ms of sustained work (measured: 163 -> 136 us per config 2
+    # forward over the first ~250 back-to-back calls, flat after that); the default warmup covers that ramp so
+    # the timed steps measure the sustained rate.
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--only", choices=["prefill", "decode"], help="run one leg only (for profiling)")
