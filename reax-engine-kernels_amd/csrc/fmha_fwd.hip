@@ -318,9 +318,6 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
 // issues all of a step's loads, one after every fourth MFMA of its MFMA phase (measured: the 32 direct-to-LDS
 // loads of a step issued by all wavefronts at the start of the step held each of them up for ~480 clocks; spread
 // this way they cost group 0 ~45 clocks each, while its matrix core work continues).
-#ifndef REAX_FWD_FA
-#define REAX_FWD_FA 0
-#endif
 constexpr int PP_NW = 8;
 #ifndef REAX_PP_STAGES
 #define REAX_PP_STAGES 2
@@ -963,15 +960,8 @@ int launch_fwd(const FwdParams& p0, int head_dim, int mode, bool post, hipStream
   // head_dim 128 qpos / varlen without the POST epilogue: the ping-pong kernel once a row tile has enough rows
   // to fill both groups (short query blocks, e.g. decode, keep the 4-wavefront kernel)
   if (head_dim == 128 && !post && p.M > FwdTile<128>::BM) {
-#if REAX_FWD_FA
-    if (mode == MODE_QPOS || mode == MODE_VARLEN) {
-      const int o_vec8 = p.o ? (aligned_elems(p.o, 4, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0) : 0;
-      return launch_fwd_fa(p, mode, o_vec8, stream);
-    }
-#else
     if (mode == MODE_QPOS) return launch_fwd_pp<MODE_QPOS>(p, stream);
     if (mode == MODE_VARLEN) return launch_fwd_pp<MODE_VARLEN>(p, stream);
-#endif
   }
   if (head_dim == 128) {
     if (mode == MODE_QPOS)

@@ -11,11 +11,6 @@ namespace reax {
 // hipErrorInvalidConfiguration for an empty grid, as the reference's zero-sized launch would report).
 int launch_fwd(const FwdParams& p, int head_dim, int mode, bool post, hipStream_t stream);
 
-// The head_dim 128 forward kernel with 64 folded rows per wavefront (MODE_QPOS or MODE_VARLEN, no gate
-// epilogue), defined in fmha_fwd_fa.hip. `p` has been validated by launch_fwd; o_vec8 = 1 when every O row
-// allows 8-byte stores.
-int launch_fwd_fa(const FwdParams& p, int mode, int o_vec8, hipStream_t stream);
-
 // Split-KV forward for short query blocks (decode): partial results per key split go to `ws`, then an LSE
 // combine kernel writes O (bf16) and the optional LSE (fmha_fwd.hip).
 struct SplitParams {

@@ -24,11 +24,8 @@ struct FwdTile {
 //     bijection on r mod 16, so the 16 units land in 16 distinct bank groups;
 //   - transposed V reads (ds_read_b64_tr_b16, 32 lanes per phase) touch 4 consecutive rows x 4 adjacent units:
 //     bits 2-3 of f() (= r & 3) differ across the 4 rows, so the 16 (row, unit) pieces are distinct.
+// Unit u of row r sits at byte r * (HD * 2) + ((u ^ swz(r)) << 4) of the tile.
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-template <int HD>
-__device__ __forceinline__ uint32_t tile_off(int r, int u) {
-  return (uint32_t)(r * (HD * 2) + ((u ^ swz(r)) << 4));
-}
 
 __device__ __forceinline__ u32x4_t ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
 
