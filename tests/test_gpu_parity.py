@@ -329,6 +329,72 @@ def test_splitkv_multitoken_d128(S, Hq, Hkv, N, splits):
     FC.check_tolerance(og, o, lg, lse, where=c.name)
 
 
+def test_splitkv_workspace_reuse():
+    """The workspace needs no initialisation: calls that share one workspace holding arbitrary bytes (different
+    splits, shapes and inputs, so a later call's partials overlap an earlier call's differently) must all be
+    right."""
+    from reax_fmha import ops
+
+    cases = [(FC.Case("reuse_a", B=4, S=1, N=3000, Hq=32, Hkv=8, D=128, mode="causal", seed=90), 16),
+             (FC.Case("reuse_b", B=2, S=2, N=777, Hq=16, Hkv=4, D=128, mode="causal", seed=91), 5),
+             (FC.Case("reuse_a2", B=4, S=1, N=3000, Hq=32, Hkv=8, D=128, mode="causal", seed=92), 16),
+             (FC.Case("reuse_c", B=8, S=1, N=2048, Hq=32, Hkv=8, D=128, mode="causal", seed=93), 16)]
+    need = max(ops.splitkv_workspace_bytes(c.B, c.Hkv, c.S * c.G, c.D, n) for c, n in cases)
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    ws = torch.randint(0, 256, (need,), dtype=torch.uint8, device="cuda", generator=gen)
+    for c, n in cases:
+        _say(f"splitkv workspace reuse {c.name} splits{n}")
+        a = FC.build(c)
+        q, k, v = dev(a["q"]), dev(a["k"]), dev(a["v"])
+        qpos = torch.from_numpy(a["qpos"]).cuda()
+        o, lse = ops.attention_splitkv(q, k, v, qpos, scale=c.scale, num_splits=n, ws=ws)
+        torch.cuda.synchronize()
+        ref_o, ref_lse = FC.oracle_ref(c, a)
+        FC.check_tolerance(host(o), ref_o, lse.cpu().numpy(), ref_lse, where=c.name)
+
+
+def test_splitkv_graph_replay():
+    """A split-KV decode (decode kernel + combine kernel) captured in a HIP graph once and replayed on new
+    inputs: every replay equals the eager call on the same inputs bit for bit, with eager calls on the same
+    workspace in between."""
+    from reax_fmha import ops
+
+    c0 = FC.Case("graph", B=2, S=1, N=1500, Hq=16, Hkv=4, D=128, mode="causal", seed=94)
+    n = 8
+    a0 = FC.build(c0)
+    q, k, v = dev(a0["q"]), dev(a0["k"]), dev(a0["v"])
+    qpos = torch.from_numpy(a0["qpos"]).cuda()
+    ws = torch.empty(ops.splitkv_workspace_bytes(c0.B, c0.Hkv, c0.G, c0.D, n), dtype=torch.uint8, device="cuda")
+    o = torch.empty_like(q)
+    lse = torch.empty((c0.B, c0.Hq, 1), dtype=torch.float32, device="cuda")
+    run = lambda: ops.attention_splitkv(q, k, v, qpos, scale=c0.scale, num_splits=n, ws=ws, o=o, lse=lse)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    torch.cuda.synchronize()
+    for i, seed in enumerate([94, 95, 96, 97]):
+        _say(f"splitkv graph replay {i} seed {seed}")
+        a = FC.build(FC.Case("graph", B=2, S=1, N=1500, Hq=16, Hkv=4, D=128, mode="causal", seed=seed))
+        q.copy_(dev(a["q"]))
+        k.copy_(dev(a["k"]))
+        v.copy_(dev(a["v"]))
+        g.replay()
+        torch.cuda.synchronize()
+        go, gl = o.clone(), lse.clone()
+        eo, el = ops.attention_splitkv(q, k, v, qpos, scale=c0.scale, num_splits=n, ws=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(go, eo) and torch.equal(gl, el), f"replay {i} differs from the eager call"
+        if i == 0:
+            ref_o, ref_lse = FC.oracle_ref(c0, a)
+            FC.check_tolerance(host(go), ref_o, gl.cpu().numpy(), ref_lse, where="graph replay")
+
+
 def test_splitkv_multitoken_d256():
     c = FC.Case("split_mt", B=2, S=3, N=700, Hq=4, Hkv=2, D=256, mode="causal", seed=82)
     _say("splitkv multi-token d256")
