@@ -6,6 +6,7 @@ pairs). A "step" is one attention forward over the resident inputs. Also reporte
   - "roofline": the forward kernel's average duration from HIP events on its stream, against 2516.6 TFLOP/s
     dense bf16 MFMA; "traffic" from the committed rocprofv3 PMC summary when present;
   - "decode": config 4 (split-KV decode + LSE combine) in HBM GB/s against 8 TB/s, L2/MALL flushed between runs;
+  - "rarn": the reduce-add RMSNorm (reax_rarn) over 8192 rows of 2560 with 4 partials, HBM GB/s against 8 TB/s;
   - "cpu_baseline": the OpenMP fp32 build of the CPU reference on a bounded sample of config 2's rows.
 Only N = 1 GPU is supported: the path is single-GPU by design.
 """
@@ -138,6 +139,36 @@ def cpu_baseline(target_s=10.0):
                        f"{flops / 1e9:.1f} GFLOP in {dt:.1f} s, fp32 OpenMP CPU reference")
 
 
+RARN_N, RARN_S = 8192, 4  # reduce-add RMSNorm leg: 8192 rows of D = 2560, 4 bf16 partials
+
+
+def bench_rarn(torch, ops, iters=20):
+    """reax_rarn over RARN_N rows with RARN_S partials, L2/MALL flushed between runs; returns (ms, GB/s) with
+    bytes = partials + residual read once, h_out + out written once (w, 5 KB, not counted)."""
+    n, S, D = RARN_N, RARN_S, 2560
+    g = torch.Generator(device="cuda").manual_seed(3)
+    part = (torch.randn(S * n * D, device="cuda", generator=g) * 0.5).to(torch.bfloat16)
+    res = torch.randn((n, D), device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(D, device="cuda", generator=g) * 0.1).to(torch.bfloat16)
+    h_out = torch.empty((n, D), dtype=torch.bfloat16, device="cuda")
+    out = torch.empty((n, D), dtype=torch.bfloat16, device="cuda")
+    run = lambda: ops.rarn(part, S, 0, n * D, res, w, n, eps=1e-6, factor=1.0 / D, h_out=h_out, out=out)
+    fl = flush_buffer(torch)
+    run()
+    ts = []
+    for _ in range(iters):
+        fl.fill_(1)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        run()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ms = float(np.median(ts))
+    nbytes = (S + 1) * n * D * 2 + 2 * n * D * 2
+    return ms, nbytes / (ms * 1e-3) / 1e9
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -148,7 +179,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode"], help="run one leg only (for profiling)")
+    ap.add_argument("--only", choices=["prefill", "decode", "rarn"], help="run one leg only (for profiling)")
+    ap.add_argument("--no-rarn", action="store_true")
     ap.add_argument("--decode-splits", type=int, default=0, help="override config 4's key-split count")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 5 times: the reference kernel for scaling "
@@ -172,6 +204,11 @@ def main():
 
     from reax_fmha import ops
 
+    if args.only == "rarn":
+        ms, gbs = bench_rarn(torch, ops)
+        print(json.dumps({"rarn_GBs": round(gbs, 1), "ms": round(ms, 4), "rows": RARN_N, "partials": RARN_S}),
+              flush=True)
+        return
     if args.only == "decode":
         dcfg, dms, gbs = bench_decode(torch, ops, args.steps, args.decode_splits)
         print(json.dumps({"decode_GBs": round(gbs, 1), "ms": round(dms, 4), "splits": dcfg.num_splits}), flush=True)
@@ -209,6 +246,12 @@ def main():
                           "bytes": dcfg.decode_bytes(), "num_splits": dcfg.num_splits,
                           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
                                        "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
+    if not args.no_rarn:
+        ms, gbs = bench_rarn(torch, ops)
+        line["rarn"] = {"workload": f"reax_rarn {RARN_N} rows x 2560, {RARN_S} partials", "value": round(gbs, 1),
+                        "unit": "GB/s", "ms": round(ms, 4),
+                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
+                                     "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

@@ -9,9 +9,10 @@
  *   1. the reference's FMHA entry points (drop-in, head_dim 256);
  *   2. extension entry points for what the reference ABI cannot express (head_dim 128, LSE output, two-stride
  *      [S][Hq][D] row addressing, packed varlen sequences, split-KV decode with an LSE combine);
- *   3. the reference's Gated-DeltaNet / norm / conv entry points, exported so that a loader which resolves every
- *      symbol still loads this library. They are not implemented here: each returns REAX_ERR_NOT_IMPLEMENTED
- *      (the *_smem queries return 0) and launches nothing.
+ *   3. the reference's Gated-DeltaNet / conv entry points, exported so that a loader which resolves every
+ *      symbol still loads this library. They are not implemented yet: each returns REAX_ERR_NOT_IMPLEMENTED
+ *      (the *_smem queries return 0) and launches nothing;
+ *   4. the reference's reduce-add RMSNorm (reax_rarn).
  */
 #ifndef LIBREAX_HOWU_H
 #define LIBREAX_HOWU_H
@@ -95,9 +96,6 @@ int reax_kkt(const void* k, const void* g, const void* beta, void* A, const void
              int HV, void* stream);
 /* libreax_howu/reax_kkt.cu:272 (returns 0 here) */
 int reax_kkt_smem(void);
-/* libreax_howu/reax_rarn_final.cu:98-106 */
-int reax_rarn(const void* part, int S, int serial, long long pstride, const void* res, const void* w, void* h_out,
-              void* out, int n, int D, float eps, float factor, void* stream);
 /* libreax_howu/reax_howu_norm_v3.cu:431-435 */
 int reax_howu_norm(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g,
                    void* out, const void* cu, float scale, int N, int H, int HV, void* stream, const void* f2s,
@@ -108,6 +106,17 @@ int reax_conv_l2(const void* qkv, long long SX, const void* cache, int C, const 
 /* libreax_howu/reax_conv_v2.cu:183-189 */
 int reax_conv_v(const void* qkv, long long SX, const void* cache, int C, const void* meta, const void* w, void* v,
                 int Tf, int KD, int VD, void* stream);
+
+/* ---- 4. reference norm entry points implemented here ---------------------------------------------------- */
+
+/* Reduce-add RMSNorm. Replaces reax_rarn, libreax_howu/reax_rarn_final.cu:98-106. Rows of D = 2560 bf16:
+ * h = bf16(res + bf16(part[0] + ... + part[S-1])) (serial != 0: rounded to bf16 after every add), written to h_out;
+ * out = bf16(h * r * (1 + w)) with r = 1/sqrt(factor * sum(h^2) + eps), the sum in the reference's fixed order.
+ * part: S partials, pstride elements apart. Returns 0 for n <= 0, -1 for D != 2560, -2 for S outside 2..8 (the
+ * reference's codes), hipErrorInvalidValue for a null buffer or rows not 4-byte aligned, else hipGetLastError().
+ * r is computed in double precision and rounded to fp32, where the reference uses the approximate rsqrtf. */
+int reax_rarn(const void* part, int S, int serial, long long pstride, const void* res, const void* w, void* h_out,
+              void* out, int n, int D, float eps, float factor, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,4 +1,4 @@
-"""ctypes binding of the CPU oracle (liboracle_fmha.so).
+"""ctypes binding of the CPU oracle (liboracle_fmha.so, and liboracle_gdn.so for the norm kernels).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke check in __graft_entry__.py and by the cpu_baseline
 leg of bench.py, always as the checker (or the timed CPU baseline), never as the product path.
@@ -15,6 +15,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle_fmha.so")
+GDN_LIB_PATH = os.path.join(HERE, "liboracle_gdn.so")
 
 MASK_QPOS, MASK_BIAS, MASK_VARLEN_CAUSAL, MASK_NONE = 0, 1, 2, 3
 
@@ -190,3 +191,39 @@ def lse_combine(part_o, part_lse):
     if rc != 0:
         raise ValueError("oracle_lse_combine rejected arguments")
     return o, lse
+
+
+# ------------------------------------------------------------------------------------------- norm kernels
+
+_gdn = None
+
+RARN_MUTANTS = {"rarn_flat_sum": 1, "rarn_no_one_plus_w": 2, "rarn_no_d_round": 3}
+
+
+def gdn_lib():
+    global _gdn
+    if _gdn is None:
+        if not os.path.exists(GDN_LIB_PATH):
+            build()
+        L = ctypes.CDLL(GDN_LIB_PATH)
+        L.oracle_rarn.restype = ctypes.c_int
+        L.oracle_rarn.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p,
+                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_float, ctypes.c_float, ctypes.c_int, ctypes.c_void_p]
+        _gdn = L
+    return _gdn
+
+
+def rarn(part, S, serial, pstride, res, w, n, *, D=2560, eps=1e-6, factor=1.0 / 2560, mutant=0):
+    """reax_rarn on the CPU: returns (code, h_out, out, r): h_out and out as uint16 bf16 bit arrays of shape (n, D),
+    r the per-row fp32 reciprocal RMS."""
+    part = np.ascontiguousarray(part, dtype=np.uint16)
+    res = np.ascontiguousarray(res, dtype=np.uint16)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    h_out = np.zeros((max(n, 0), D), dtype=np.uint16)
+    out = np.zeros((max(n, 0), D), dtype=np.uint16)
+    r = np.zeros(max(n, 0), dtype=np.float32)
+    m = RARN_MUTANTS.get(mutant, mutant) if isinstance(mutant, str) else mutant
+    code = gdn_lib().oracle_rarn(_ptr(part), S, int(serial), pstride, _ptr(res), _ptr(w), _ptr(h_out), _ptr(out),
+                                 n, D, ctypes.c_float(eps), ctypes.c_float(factor), m, _ptr(r))
+    return code, h_out, out, r

@@ -1,7 +1,7 @@
-// Gated-DeltaNet / norm / conv entry points of libreax_howu.so that are outside the attention path.
-// They keep the reference prototypes (libreax_howu/reax_howu.cu:363-376, reax_kkt.cu:263-272,
-// reax_rarn_final.cu:98-106, reax_howu_norm_v3.cu:431-435, reax_conv_v2.cu:164-189) so that a loader which
-// resolves every symbol of the library still loads it, but launch nothing and return REAX_ERR_NOT_IMPLEMENTED.
+// Gated-DeltaNet / norm / conv entry points of libreax_howu.so that are not implemented yet. They keep the
+// reference prototypes (libreax_howu/reax_howu.cu:363-376, reax_kkt.cu:263-272, reax_howu_norm_v3.cu:431-435,
+// reax_conv_v2.cu:164-189) so that a loader which resolves every symbol of the library still loads it, but launch
+// nothing and return REAX_ERR_NOT_IMPLEMENTED. (reax_rarn is implemented in gdn_rarn.hip.)
 #pragma GCC visibility push(default)
 #include "libreax_howu.h"
 #pragma GCC visibility pop
@@ -25,10 +25,6 @@ int reax_kkt(const void*, const void*, const void*, void*, const void*, const vo
   return REAX_ERR_NOT_IMPLEMENTED;
 }
 int reax_kkt_smem(void) { return 0; }
-int reax_rarn(const void*, int, int, long long, const void*, const void*, void*, void*, int, int, float, float,
-              void*) {
-  return REAX_ERR_NOT_IMPLEMENTED;
-}
 int reax_howu_norm(const void*, const void*, const void*, const void*, const void*, const void*, void*, const void*,
                    float, int, int, int, void*, const void*, const void*, long long, const void*, float, float) {
   return REAX_ERR_NOT_IMPLEMENTED;

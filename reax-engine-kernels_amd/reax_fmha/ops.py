@@ -148,3 +148,17 @@ def attention_splitkv(q, k, v, qpos, *, scale, num_splits, ws=None, o=None, lse=
         ls[0], G * ls[1], ls[2], ls[1], _stream())
     _check("reax_fmha_splitkv", rc)
     return o, lse
+
+
+def rarn(part, S, serial, pstride, res, w, n, *, eps, factor, h_out=None, out=None, D=2560):
+    """reax_rarn (libreax_howu/reax_rarn_final.cu:98-106) on device tensors: part is a bf16 buffer holding S
+    partials of (n, D) rows, pstride elements apart; res (n, D), w (D,). Returns (h_out, out), each (n, D) bf16."""
+    _dev(part, res, w)
+    if h_out is None:
+        h_out = torch.empty((max(n, 1), D), dtype=torch.bfloat16, device=res.device)
+    if out is None:
+        out = torch.empty((max(n, 1), D), dtype=torch.bfloat16, device=res.device)
+    rc = abi.howu().reax_rarn(part.data_ptr(), S, int(serial), pstride, res.data_ptr(), w.data_ptr(),
+                              h_out.data_ptr(), out.data_ptr(), n, D, eps, factor, _stream())
+    _check("reax_rarn", rc)
+    return h_out, out

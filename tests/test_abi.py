@@ -61,8 +61,20 @@ def test_gdn_entry_points_not_implemented():
     assert L.howu3_smem() == 0 and L.reax_kkt_smem() == 0
     assert L.reax_howu(*([None] * 8 + [1.0, 1, 1, 1, None])) == abi.REAX_ERR_NOT_IMPLEMENTED
     assert L.reax_kkt(*([None] * 6 + [1, 1, 2, None])) == abi.REAX_ERR_NOT_IMPLEMENTED
-    assert L.reax_rarn(None, 2, 0, 0, None, None, None, None, 1, 2560, 1e-6, 1.0, None) == abi.REAX_ERR_NOT_IMPLEMENTED
     assert L.reax_conv_v(None, 0, None, 0, None, None, None, 1, 128, 128, None) == abi.REAX_ERR_NOT_IMPLEMENTED
+
+
+def test_rarn_argument_codes():
+    # reax_rarn (rarn_final.cu:100, 104): n <= 0 -> 0 (even with a wrong D), D != 2560 -> -1, S outside 2..8 -> -2;
+    # a missing buffer (which the reference would fault on) -> hipErrorInvalidValue; none of these launches
+    L = abi.howu()
+    args = lambda S, n, D: (None, S, 0, 0, None, None, None, None, n, D, 1e-6, 1.0 / 2560, None)
+    assert L.reax_rarn(*args(2, 0, 2560)) == 0
+    assert L.reax_rarn(*args(2, -3, 100)) == 0
+    assert L.reax_rarn(*args(2, 4, 2048)) == -1
+    assert L.reax_rarn(*args(1, 4, 2560)) == -2
+    assert L.reax_rarn(*args(9, 4, 2560)) == -2
+    assert L.reax_rarn(*args(4, 4, 2560)) == 1  # hipErrorInvalidValue
 
 
 def test_splitkv_workspace_size():
