@@ -7,6 +7,7 @@ pairs). A "step" is one attention forward over the resident inputs. Also reporte
     dense bf16 MFMA; "traffic" from the committed rocprofv3 PMC summary when present;
   - "decode": config 4 (split-KV decode + LSE combine) in HBM GB/s against 8 TB/s, L2/MALL flushed between runs;
   - "rarn": the reduce-add RMSNorm (reax_rarn) over 8192 rows of 2560 with 4 partials, HBM GB/s against 8 TB/s;
+  - "conv": the causal conv + SiLU + L2 norm (reax_conv_l2, rep 2) over 4096 tokens, HBM GB/s against 8 TB/s;
   - "cpu_baseline": the OpenMP fp32 build of the CPU reference on a bounded sample of config 2's rows.
 Only N = 1 GPU is supported: the path is single-GPU by design.
 """
@@ -169,6 +170,42 @@ def bench_rarn(torch, ops, iters=20):
     return ms, nbytes / (ms * 1e-3) / 1e9
 
 
+CONV_T, CONV_KD, CONV_VD = 4096, 2048, 4096  # conv + SiLU + L2 leg: 4096 new tokens, 16 q/k heads, 32 v heads
+
+
+def bench_conv(torch, ops, iters=20):
+    """reax_conv_l2 (rep 2) over CONV_T tokens of one sequence with 3 cached positions, L2/MALL flushed between runs;
+    returns (ms, GB/s) with bytes = qkv read once + q, k (both copies), v written once (weights, cache, meta not
+    counted)."""
+    T, KD, VD = CONV_T, CONV_KD, CONV_VD
+    ch = 2 * KD + VD
+    g = torch.Generator(device="cuda").manual_seed(4)
+    qkv = torch.randn((T, ch), device="cuda", generator=g).to(torch.bfloat16)
+    cache = torch.randn((3, ch), device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn((ch, 4), device="cuda", generator=g) * 0.5).to(torch.bfloat16)
+    pos = torch.arange(T, dtype=torch.int32, device="cuda") + 3
+    meta = torch.stack([pos, torch.full_like(pos, 3), torch.full_like(pos, -3), torch.zeros_like(pos)], 1)
+    meta = meta.contiguous()
+    q = torch.empty((T, 2 * KD), dtype=torch.bfloat16, device="cuda")
+    k = torch.empty_like(q)
+    v = torch.empty((T, VD), dtype=torch.bfloat16, device="cuda")
+    run = lambda: ops.conv_l2(qkv, cache, meta, w, Tf=T, KD=KD, VD=VD, eps=1e-6, rep=2, q=q, k=k, v=v)
+    fl = flush_buffer(torch)
+    run()
+    ts = []
+    for _ in range(iters):
+        fl.fill_(1)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        run()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ms = float(np.median(ts))
+    nbytes = T * ch * 2 + 2 * T * 2 * KD * 2 + T * VD * 2
+    return ms, nbytes / (ms * 1e-3) / 1e9
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -179,8 +216,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "rarn"], help="run one leg only (for profiling)")
-    ap.add_argument("--no-rarn", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "decode", "rarn", "conv"], help="run one leg only (for profiling)")
+    ap.add_argument("--no-gdn", action="store_true", help="skip the reax_rarn and reax_conv_l2 legs")
     ap.add_argument("--decode-splits", type=int, default=0, help="override config 4's key-split count")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 5 times: the reference kernel for scaling "
@@ -204,6 +241,10 @@ def main():
 
     from reax_fmha import ops
 
+    if args.only == "conv":
+        ms, gbs = bench_conv(torch, ops)
+        print(json.dumps({"conv_GBs": round(gbs, 1), "ms": round(ms, 4), "tokens": CONV_T}), flush=True)
+        return
     if args.only == "rarn":
         ms, gbs = bench_rarn(torch, ops)
         print(json.dumps({"rarn_GBs": round(gbs, 1), "ms": round(ms, 4), "rows": RARN_N, "partials": RARN_S}),
@@ -246,10 +287,15 @@ def main():
                           "bytes": dcfg.decode_bytes(), "num_splits": dcfg.num_splits,
                           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
                                        "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
-    if not args.no_rarn:
+    if not args.no_gdn:
         ms, gbs = bench_rarn(torch, ops)
         line["rarn"] = {"workload": f"reax_rarn {RARN_N} rows x 2560, {RARN_S} partials", "value": round(gbs, 1),
                         "unit": "GB/s", "ms": round(ms, 4),
+                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
+                                     "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
+        ms, gbs = bench_conv(torch, ops)
+        line["conv"] = {"workload": f"reax_conv_l2 {CONV_T} tokens, KD {CONV_KD}, VD {CONV_VD}, rep 2",
+                        "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
                         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
                                      "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
     if not args.no_cpu:

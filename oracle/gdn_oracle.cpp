@@ -1,11 +1,11 @@
-// CPU oracle for the norm kernels of libreax_howu.so outside the attention path.
+// CPU oracle for the norm and conv kernels of libreax_howu.so outside the attention path.
 //
 // TEST INFRASTRUCTURE ONLY. This file is the checker, never the product: only tests/ (and the smoke check in
 // __graft_entry__.py) may load the library built from it. It is compiled with -ffp-contract=off so that every
 // fp32 operation below rounds exactly as written (the reference is built with nvcc -fmad=false, build.sh:17-18).
 //
-// rarn_ref restates libreax_howu/reax_rarn_final.cu (reduce-add RMSNorm, D = 2560), element by element, in the
-// reference's rounding order:
+// oracle_rarn restates libreax_howu/reax_rarn_final.cu ("rarn" below; reduce-add RMSNorm, D = 2560), element by
+// element, in the reference's rounding order:
 //   d = part[0]; d = d + part[s] for s = 1..S-1 (serial: bf16 round after every add); d = bf16(d)  (rarn:47-54)
 //   h = bf16(res + d)                                                                               (rarn:55)
 //   a[c] = sum over chunks k = 0..19 in order of h[128k + c]^2, c = 0..127 (product rounded)        (rarn:57-58)
@@ -15,6 +15,20 @@
 //   out = bf16((h * r) * (1 + w))                                                                    (rarn:86-87)
 // The reference evaluates r with CUDA's approximate rsqrtf; this oracle (like the HIP kernel) evaluates it in
 // double precision and rounds to fp32: bit-exact agreement with the reference at that step is not claimed.
+//
+// oracle_conv restates libreax_howu/reax_conv_v2.cu ("conv" below; causal 4-tap conv1d + SiLU + L2 norm):
+//   tap j = 0..3: src = meta.x - 3 + j, skipped when src < 0; row meta.z + src of qkv when src >= meta.y, else row
+//   meta.w + src of the cache                                                                        (conv:88-92)
+//   acc = fma(w[c][j], x, acc) over the taps in order, from 0                                        (conv:96-108)
+//   y = bf16(acc); s = bf16(y / fp32(1 + exp(-y)))                                                   (conv:112-122)
+//   q/k units: per 8-channel group p = s1*s1, then fma(s0, s0, p), fma(s2, s2, p) .. fma(s7, s7, p); the 16 groups
+//   of a 128-channel unit combine by a butterfly over group distance 8, 4, 2, 1; rstd = 1 / sqrt(eps + sum);
+//   out = bf16(rstd * s), written once (rep 1) or twice side by side (rep 2)                         (conv:123-142)
+//   v units: out = s                                                                                 (conv:143-147)
+// The reference evaluates exp, sqrt and the reciprocal with fast approximations (its exp restates libdevice's
+// expf, which this project does not reproduce); the oracle, like the HIP kernel, evaluates 1 + exp(-y) and
+// 1/sqrt in double precision and rounds them to fp32, so bit-exact agreement with the reference is not claimed
+// for those steps.
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -90,6 +104,73 @@ int oracle_rarn(const uint16_t* part, int S, int serial, long long pstride, cons
       const float wv = bf2f(w[c]);
       const float g = mutant == 2 ? wv : 1.f + wv;
       out[ro + c] = f2bf((hrow[c] * r) * g);
+    }
+  }
+  return 0;
+}
+
+// Returns 0. units q/k: u < 2*KD/128 (q: u < KD/128); v: the rest. rstd_out (may be null): [Tf][2*KD/128].
+// mutant != 0 plants a deliberate mistake (used only to show that the pinning tests catch it):
+//   1: taps applied in reverse order (w[c][3 - j] with tap j)
+//   2: a source row equal to meta.y taken from the cache instead of qkv
+//   3: the L2 sum accumulated over the 128 channels in plain order
+//   4: SiLU with the sign flipped inside the exponential
+int oracle_conv(const uint16_t* qkv, long long SX, const uint16_t* cache, int C, const int* meta, const uint16_t* w,
+                uint16_t* q, uint16_t* k, uint16_t* v, int Tf, float eps, int KD, int VD, int rep, int skip_v, int u0,
+                int units, int mutant, float* rstd_out) {
+  const int nqk = 2 * KD / 128, nq = KD / 128;
+  for (int t = 0; t < Tf; ++t) {
+    const int* m = meta + 4LL * t;
+    for (int u = u0; u < u0 + units; ++u) {
+      float s[128];
+      for (int c = 0; c < 128; ++c) {
+        const long long ch = 128LL * u + c;
+        float acc = 0.f;
+        for (int j = 0; j < 4; ++j) {
+          const int src = m[0] - 3 + j;
+          if (src < 0) continue;
+          const bool from_qkv = mutant == 2 ? src > m[1] : src >= m[1];
+          const uint16_t xb = from_qkv ? qkv[(long long)(m[2] + src) * SX + ch] : cache[(long long)(m[3] + src) * C + ch];
+          const int jw = mutant == 1 ? 3 - j : j;
+          acc = std::fmaf(bf2f(w[ch * 4 + jw]), bf2f(xb), acc);
+        }
+        const float y = bfr(acc);
+        const float d = (float)(1.0 + std::exp(mutant == 4 ? (double)y : -(double)y));
+        s[c] = bfr(y / d);
+      }
+      if (u < nqk) {
+        float sum;
+        if (mutant == 3) {
+          sum = 0.f;
+          for (int c = 0; c < 128; ++c) sum = std::fmaf(s[c], s[c], sum);
+        } else {
+          float g[16];
+          for (int l = 0; l < 16; ++l) {
+            const float* x = s + 8 * l;
+            float p = x[1] * x[1];
+            p = std::fmaf(x[0], x[0], p);
+            for (int i = 2; i < 8; ++i) p = std::fmaf(x[i], x[i], p);
+            g[l] = p;
+          }
+          for (int dist = 8; dist >= 1; dist >>= 1) {
+            float h[16];
+            for (int l = 0; l < 16; ++l) h[l] = g[l] + g[l ^ dist];
+            for (int l = 0; l < 16; ++l) g[l] = h[l];
+          }
+          sum = g[0];
+        }
+        const float rstd = (float)(1.0 / std::sqrt((double)(eps + sum)));
+        if (rstd_out) rstd_out[(long long)t * nqk + u] = rstd;
+        const int REP = rep == 1 ? 1 : 2, nh = REP * KD / 128, hq = u % nq;
+        uint16_t* dst = (u < nq ? q : k) + (long long)t * (nh * 128) + REP * hq * 128;
+        for (int c = 0; c < 128; ++c) {
+          dst[c] = f2bf(rstd * s[c]);
+          if (REP == 2) dst[128 + c] = dst[c];
+        }
+      } else if (!skip_v) {
+        uint16_t* dst = v + (long long)t * VD + (128LL * u - 2 * KD);
+        for (int c = 0; c < 128; ++c) dst[c] = f2bf(s[c]);
+      }
     }
   }
   return 0;

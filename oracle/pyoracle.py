@@ -227,3 +227,36 @@ def rarn(part, S, serial, pstride, res, w, n, *, D=2560, eps=1e-6, factor=1.0 / 
     code = gdn_lib().oracle_rarn(_ptr(part), S, int(serial), pstride, _ptr(res), _ptr(w), _ptr(h_out), _ptr(out),
                                  n, D, ctypes.c_float(eps), ctypes.c_float(factor), m, _ptr(r))
     return code, h_out, out, r
+
+
+CONV_MUTANTS = {"conv_taps_reversed": 1, "conv_route_strict": 2, "conv_flat_l2": 3, "conv_silu_sign": 4}
+
+
+def conv(qkv, SX, cache, C, meta, w, Tf, *, KD, VD, eps=1e-6, rep=1, skip_v=0, u0=0, units=None, mutant=0):
+    """reax_conv_l2 / reax_conv_v on the CPU. qkv, cache, w: bf16 bit arrays; meta: int32 [Tf][4].
+    Returns (q, k, v, rstd): q, k of shape (Tf, rep*KD) and v (Tf, VD) as bf16 bits (zeros where not written),
+    rstd (Tf, 2*KD/128) fp32."""
+    L = gdn_lib()
+    if not hasattr(L, "_conv_typed"):
+        L.oracle_conv.restype = ctypes.c_int
+        L.oracle_conv.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                  ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+        L._conv_typed = True
+    qkv = np.ascontiguousarray(qkv, dtype=np.uint16)
+    cache = np.ascontiguousarray(cache, dtype=np.uint16)
+    meta = np.ascontiguousarray(meta, dtype=np.int32)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    REP = 1 if rep == 1 else 2
+    q = np.zeros((Tf, REP * KD), dtype=np.uint16)
+    k = np.zeros((Tf, REP * KD), dtype=np.uint16)
+    v = np.zeros((Tf, max(VD, 1)), dtype=np.uint16)
+    nqk = 2 * KD // 128
+    rstd = np.zeros((Tf, nqk), dtype=np.float32)
+    if units is None:
+        units = nqk + (0 if skip_v else VD // 128)
+    m = CONV_MUTANTS.get(mutant, mutant) if isinstance(mutant, str) else mutant
+    L.oracle_conv(_ptr(qkv), SX, _ptr(cache), C, _ptr(meta), _ptr(w), _ptr(q), _ptr(k), _ptr(v), Tf,
+                  ctypes.c_float(eps), KD, VD, rep, skip_v, u0, units, m, _ptr(rstd))
+    return q, k, v, rstd

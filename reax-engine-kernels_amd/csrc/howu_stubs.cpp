@@ -1,7 +1,7 @@
 // Gated-DeltaNet / norm / conv entry points of libreax_howu.so that are not implemented yet. They keep the
-// reference prototypes (libreax_howu/reax_howu.cu:363-376, reax_kkt.cu:263-272, reax_howu_norm_v3.cu:431-435,
-// reax_conv_v2.cu:164-189) so that a loader which resolves every symbol of the library still loads it, but launch
-// nothing and return REAX_ERR_NOT_IMPLEMENTED. (reax_rarn is implemented in gdn_rarn.hip.)
+// reference prototypes (libreax_howu/reax_howu.cu:363-376, reax_kkt.cu:263-272, reax_howu_norm_v3.cu:431-435) so
+// that a loader which resolves every symbol of the library still loads it, but launch nothing and return
+// REAX_ERR_NOT_IMPLEMENTED. (reax_rarn is implemented in gdn_rarn.hip, reax_conv_l2 / reax_conv_v in gdn_conv.hip.)
 #pragma GCC visibility push(default)
 #include "libreax_howu.h"
 #pragma GCC visibility pop
@@ -29,12 +29,4 @@ int reax_howu_norm(const void*, const void*, const void*, const void*, const voi
                    float, int, int, int, void*, const void*, const void*, long long, const void*, float, float) {
   return REAX_ERR_NOT_IMPLEMENTED;
 }
-int reax_conv_l2(const void*, long long, const void*, int, const void*, const void*, void*, void*, void*, int, float,
-                 int, int, int, int, int, void*) {
-  return REAX_ERR_NOT_IMPLEMENTED;
-}
-int reax_conv_v(const void*, long long, const void*, int, const void*, const void*, void*, int, int, int, void*) {
-  return REAX_ERR_NOT_IMPLEMENTED;
-}
-
 }  // extern "C"

@@ -162,3 +162,29 @@ def rarn(part, S, serial, pstride, res, w, n, *, eps, factor, h_out=None, out=No
                               h_out.data_ptr(), out.data_ptr(), n, D, eps, factor, _stream())
     _check("reax_rarn", rc)
     return h_out, out
+
+
+def conv_l2(qkv, cache, meta, w, *, Tf, KD, VD, eps, rep=1, skip_v=0, RT=16, q=None, k=None, v=None):
+    """reax_conv_l2 (libreax_howu/reax_conv_v2.cu:164-181) on device tensors: qkv (rows, SX) and cache (rows, C)
+    bf16, meta int32 (Tf, 4), w bf16 (2*KD + VD, 4). Returns (q, k, v): q, k (Tf, rep*KD), v (Tf, VD) bf16."""
+    _dev(qkv, cache, meta, w)
+    REP = 1 if rep == 1 else 2
+    dev = qkv.device
+    q = torch.empty((max(Tf, 1), REP * KD), dtype=torch.bfloat16, device=dev) if q is None else q
+    k = torch.empty((max(Tf, 1), REP * KD), dtype=torch.bfloat16, device=dev) if k is None else k
+    v = torch.empty((max(Tf, 1), max(VD, 1)), dtype=torch.bfloat16, device=dev) if v is None else v
+    rc = abi.howu().reax_conv_l2(qkv.data_ptr(), qkv.stride(0), cache.data_ptr(), cache.stride(0), meta.data_ptr(),
+                                 w.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), Tf, eps, KD, VD, rep, skip_v,
+                                 RT, _stream())
+    _check("reax_conv_l2", rc)
+    return q, k, v
+
+
+def conv_v(qkv, cache, meta, w, *, Tf, KD, VD, v=None):
+    """reax_conv_v (libreax_howu/reax_conv_v2.cu:183-189): the value channels only. Returns v (Tf, VD) bf16."""
+    _dev(qkv, cache, meta, w)
+    v = torch.empty((max(Tf, 1), VD), dtype=torch.bfloat16, device=qkv.device) if v is None else v
+    rc = abi.howu().reax_conv_v(qkv.data_ptr(), qkv.stride(0), cache.data_ptr(), cache.stride(0), meta.data_ptr(),
+                                w.data_ptr(), v.data_ptr(), Tf, KD, VD, _stream())
+    _check("reax_conv_v", rc)
+    return v

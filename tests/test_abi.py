@@ -61,7 +61,6 @@ def test_gdn_entry_points_not_implemented():
     assert L.howu3_smem() == 0 and L.reax_kkt_smem() == 0
     assert L.reax_howu(*([None] * 8 + [1.0, 1, 1, 1, None])) == abi.REAX_ERR_NOT_IMPLEMENTED
     assert L.reax_kkt(*([None] * 6 + [1, 1, 2, None])) == abi.REAX_ERR_NOT_IMPLEMENTED
-    assert L.reax_conv_v(None, 0, None, 0, None, None, None, 1, 128, 128, None) == abi.REAX_ERR_NOT_IMPLEMENTED
 
 
 def test_rarn_argument_codes():
@@ -75,6 +74,19 @@ def test_rarn_argument_codes():
     assert L.reax_rarn(*args(1, 4, 2560)) == -2
     assert L.reax_rarn(*args(9, 4, 2560)) == -2
     assert L.reax_rarn(*args(4, 4, 2560)) == 1  # hipErrorInvalidValue
+
+
+def test_conv_argument_codes():
+    # reax_conv_l2 / reax_conv_v (conv_v2:166, 173-177, 185): Tf <= 0 -> 0, RT outside {8, 16, 32} -> -1; missing
+    # buffers (which the reference would fault on) -> hipErrorInvalidValue; none of these launches
+    L = abi.howu()
+    l2 = lambda Tf, RT: (None, 0, None, 0, None, None, None, None, None, Tf, 1e-6, 128, 128, 1, 0, RT, None)
+    assert L.reax_conv_l2(*l2(0, 16)) == 0
+    assert L.reax_conv_l2(*l2(0, 7)) == 0
+    assert L.reax_conv_l2(*l2(4, 12)) == -1
+    assert L.reax_conv_l2(*l2(4, 16)) == 1
+    assert L.reax_conv_v(None, 0, None, 0, None, None, None, 0, 128, 128, None) == 0
+    assert L.reax_conv_v(None, 0, None, 0, None, None, None, 3, 128, 128, None) == 1
 
 
 def test_splitkv_workspace_size():
