@@ -9,10 +9,10 @@
  *   1. the reference's FMHA entry points (drop-in, head_dim 256);
  *   2. extension entry points for what the reference ABI cannot express (head_dim 128, LSE output, two-stride
  *      [S][Hq][D] row addressing, packed varlen sequences, split-KV decode with an LSE combine);
- *   3. the reference's Gated-DeltaNet / conv entry points, exported so that a loader which resolves every
+ *   3. the reference's Gated-DeltaNet chunk entry points, exported so that a loader which resolves every
  *      symbol still loads this library. They are not implemented yet: each returns REAX_ERR_NOT_IMPLEMENTED
  *      (the *_smem queries return 0) and launches nothing;
- *   4. the reference's reduce-add RMSNorm (reax_rarn).
+ *   4. the reference's reduce-add RMSNorm (reax_rarn) and causal conv + SiLU + L2 norm (reax_conv_l2, reax_conv_v).
  */
 #ifndef LIBREAX_HOWU_H
 #define LIBREAX_HOWU_H
@@ -100,14 +100,7 @@ int reax_kkt_smem(void);
 int reax_howu_norm(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g,
                    void* out, const void* cu, float scale, int N, int H, int HV, void* stream, const void* f2s,
                    const void* z, long long ZS, const void* nw, float eps, float factor);
-/* libreax_howu/reax_conv_v2.cu:164-181 */
-int reax_conv_l2(const void* qkv, long long SX, const void* cache, int C, const void* meta, const void* w, void* q,
-                 void* k, void* v, int Tf, float eps, int KD, int VD, int rep, int skip_v, int RT, void* stream);
-/* libreax_howu/reax_conv_v2.cu:183-189 */
-int reax_conv_v(const void* qkv, long long SX, const void* cache, int C, const void* meta, const void* w, void* v,
-                int Tf, int KD, int VD, void* stream);
-
-/* ---- 4. reference norm entry points implemented here ---------------------------------------------------- */
+/* ---- 4. reference norm / conv entry points implemented here --------------------------------------------- */
 
 /* Reduce-add RMSNorm. Replaces reax_rarn, libreax_howu/reax_rarn_final.cu:98-106. Rows of D = 2560 bf16:
  * h = bf16(res + bf16(part[0] + ... + part[S-1])) (serial != 0: rounded to bf16 after every add), written to h_out;
@@ -117,6 +110,24 @@ int reax_conv_v(const void* qkv, long long SX, const void* cache, int C, const v
  * r is computed in double precision and rounded to fp32, where the reference uses the approximate rsqrtf. */
 int reax_rarn(const void* part, int S, int serial, long long pstride, const void* res, const void* w, void* h_out,
               void* out, int n, int D, float eps, float factor, void* stream);
+
+/* Causal 4-tap conv1d + SiLU + per-head L2 norm of q/k. Replaces reax_conv_l2, libreax_howu/reax_conv_v2.cu:164-181.
+ * Token t (meta[t] = {position, first position held by qkv, qkv row offset, cache row offset}) reads source
+ * positions position-3 .. position (skipping negative ones) from qkv (row stride SX) or the conv cache (row stride
+ * C); channels form 128-wide units: KD/128 q heads, KD/128 k heads, then VD/128 v heads; w is [2*KD + VD][4] bf16.
+ * q/k: bf16(s * rstd) with rstd = 1/sqrt(eps + sum of s^2 over the head), written once (rep 1) or twice side by side
+ * (rep != 1) into q/k rows of rep*KD; v (unless skip_v): s, rows of VD. s = bf16(y / (1 + exp(-y))), y = bf16(conv).
+ * Returns 0 for Tf <= 0, -1 for RT outside {8, 16, 32} (the reference's codes; RT is its tiling choice and only
+ * checked here), hipErrorInvalidValue for missing buffers, KD not a positive multiple of 128, VD not a multiple of
+ * 128, or rows / meta / outputs not 16-byte aligned, weights not 8-byte aligned; else hipGetLastError(). qkv must
+ * hold at least one row. exp and 1/sqrt are evaluated to fp32 accuracy where the reference uses CUDA's fast
+ * approximations: a bf16 result can differ from the reference's by one ulp in rare elements. */
+int reax_conv_l2(const void* qkv, long long SX, const void* cache, int C, const void* meta, const void* w, void* q,
+                 void* k, void* v, int Tf, float eps, int KD, int VD, int rep, int skip_v, int RT, void* stream);
+/* The value units only (v = s, no q/k outputs). Replaces reax_conv_v, libreax_howu/reax_conv_v2.cu:183-189.
+ * Returns 0 for Tf <= 0, hipErrorInvalidValue as reax_conv_l2, else hipGetLastError(). */
+int reax_conv_v(const void* qkv, long long SX, const void* cache, int C, const void* meta, const void* w, void* v,
+                int Tf, int KD, int VD, void* stream);
 
 #ifdef __cplusplus
 }
