@@ -8,6 +8,7 @@ pairs). A "step" is one attention forward over the resident inputs. Also reporte
   - "decode": config 4 (split-KV decode + LSE combine) in HBM GB/s against 8 TB/s, L2/MALL flushed between runs;
   - "rarn": the reduce-add RMSNorm (reax_rarn) over 8192 rows of 2560 with 4 partials, HBM GB/s against 8 TB/s;
   - "conv": the causal conv + SiLU + L2 norm (reax_conv_l2, rep 2) over 4096 tokens, HBM GB/s against 8 TB/s;
+  - "kkt": the GDN chunk solve (reax_kkt) over 8192 tokens x 16 key heads, GB/s of k read + A written;
   - "cpu_baseline": the OpenMP fp32 build of the CPU reference on a bounded sample of config 2's rows.
 Only N = 1 GPU is supported: the path is single-GPU by design.
 """
@@ -206,6 +207,40 @@ def bench_conv(torch, ops, iters=20):
     return ms, nbytes / (ms * 1e-3) / 1e9
 
 
+KKT_T, KKT_H = 8192, 16  # chunk-solve leg: one sequence of 8192 tokens, 16 key heads (32 value heads)
+
+
+def bench_kkt(torch, ops, iters=20):
+    """reax_kkt over KKT_T tokens (128 chunks of 64) x KKT_H key heads, L2/MALL flushed between runs; returns
+    (ms, GB/s) with bytes = k read once + A written once (g, beta not counted)."""
+    T, H = KKT_T, KKT_H
+    HV = 2 * H
+    g_ = torch.Generator(device="cuda").manual_seed(5)
+    k = torch.randn((T, H, 128), device="cuda", generator=g_)
+    k = (k / k.norm(dim=2, keepdim=True)).to(torch.bfloat16)
+    g = torch.cumsum(-torch.rand((T, HV), device="cuda", generator=g_) * 0.2, 0).float()
+    beta = torch.sigmoid(torch.randn((T, HV), device="cuda", generator=g_)).to(torch.bfloat16)
+    cu = torch.tensor([0, T], dtype=torch.int64, device="cuda")
+    NT = T // 64
+    cidx = torch.stack([torch.zeros(NT, dtype=torch.int64), torch.arange(NT, dtype=torch.int64)], 1).cuda()
+    A = torch.zeros((T, HV, 64), dtype=torch.bfloat16, device="cuda")
+    run = lambda: ops.kkt(k, g, beta, cu, cidx, NT=NT, H=H, HV=HV, A=A)
+    fl = flush_buffer(torch)
+    run()
+    ts = []
+    for _ in range(iters):
+        fl.fill_(1)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        run()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ms = float(np.median(ts))
+    nbytes = T * H * 128 * 2 + T * HV * 64 * 2
+    return ms, nbytes / (ms * 1e-3) / 1e9
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -216,8 +251,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "rarn", "conv"], help="run one leg only (for profiling)")
-    ap.add_argument("--no-gdn", action="store_true", help="skip the reax_rarn and reax_conv_l2 legs")
+    ap.add_argument("--only", choices=["prefill", "decode", "rarn", "conv", "kkt"], help="run one leg only (for profiling)")
+    ap.add_argument("--no-gdn", action="store_true", help="skip the reax_rarn, reax_conv_l2 and reax_kkt legs")
     ap.add_argument("--decode-splits", type=int, default=0, help="override config 4's key-split count")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 5 times: the reference kernel for scaling "
@@ -241,6 +276,11 @@ def main():
 
     from reax_fmha import ops
 
+    if args.only == "kkt":
+        ms, gbs = bench_kkt(torch, ops)
+        print(json.dumps({"kkt_GBs": round(gbs, 1), "ms": round(ms, 4), "tokens": KKT_T, "key_heads": KKT_H}),
+              flush=True)
+        return
     if args.only == "conv":
         ms, gbs = bench_conv(torch, ops)
         print(json.dumps({"conv_GBs": round(gbs, 1), "ms": round(ms, 4), "tokens": CONV_T}), flush=True)
@@ -298,6 +338,11 @@ def main():
                         "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
                         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
                                      "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
+        ms, gbs = bench_kkt(torch, ops)
+        line["kkt"] = {"workload": f"reax_kkt {KKT_T} tokens, {KKT_H} key heads", "value": round(gbs, 1),
+                       "unit": "GB/s", "ms": round(ms, 4),
+                       "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
+                                    "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

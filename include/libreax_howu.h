@@ -12,7 +12,8 @@
  *   3. the reference's Gated-DeltaNet chunk entry points, exported so that a loader which resolves every
  *      symbol still loads this library. They are not implemented yet: each returns REAX_ERR_NOT_IMPLEMENTED
  *      (the *_smem queries return 0) and launches nothing;
- *   4. the reference's reduce-add RMSNorm (reax_rarn) and causal conv + SiLU + L2 norm (reax_conv_l2, reax_conv_v).
+ *   4. the reference's reduce-add RMSNorm (reax_rarn), causal conv + SiLU + L2 norm (reax_conv_l2, reax_conv_v)
+ *      and Gated-DeltaNet chunk solve (reax_kkt, reax_kkt_smem).
  */
 #ifndef LIBREAX_HOWU_H
 #define LIBREAX_HOWU_H
@@ -91,16 +92,11 @@ int howu3_smem(void);
 /* libreax_howu/reax_howu.cu:373-376 */
 int reax_howu(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g, void* o,
               const void* cu, float scale, int N, int H, int HV, void* stream);
-/* libreax_howu/reax_kkt.cu:263-271 */
-int reax_kkt(const void* k, const void* g, const void* beta, void* A, const void* cu, const void* cidx, int NT, int H,
-             int HV, void* stream);
-/* libreax_howu/reax_kkt.cu:272 (returns 0 here) */
-int reax_kkt_smem(void);
 /* libreax_howu/reax_howu_norm_v3.cu:431-435 */
 int reax_howu_norm(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g,
                    void* out, const void* cu, float scale, int N, int H, int HV, void* stream, const void* f2s,
                    const void* z, long long ZS, const void* nw, float eps, float factor);
-/* ---- 4. reference norm / conv entry points implemented here --------------------------------------------- */
+/* ---- 4. reference GDN-side entry points implemented here ------------------------------------------------ */
 
 /* Reduce-add RMSNorm. Replaces reax_rarn, libreax_howu/reax_rarn_final.cu:98-106. Rows of D = 2560 bf16:
  * h = bf16(res + bf16(part[0] + ... + part[S-1])) (serial != 0: rounded to bf16 after every add), written to h_out;
@@ -128,6 +124,19 @@ int reax_conv_l2(const void* qkv, long long SX, const void* cache, int C, const 
  * Returns 0 for Tf <= 0, hipErrorInvalidValue as reax_conv_l2, else hipGetLastError(). */
 int reax_conv_v(const void* qkv, long long SX, const void* cache, int C, const void* meta, const void* w, void* v,
                 int Tf, int KD, int VD, void* stream);
+
+/* Gated-DeltaNet chunk solve. Replaces reax_kkt, libreax_howu/reax_kkt.cu:263-271. For chunk n (cidx[2n] = sequence,
+ * cidx[2n+1] = 64-token chunk of it; cu = int64 sequence starts) and key head kh, for value heads hv = 2kh, 2kh+1:
+ * A = (I + M)^-1 with M[r][c] = (k_r . k_c) * 2^(g[r] - g[c]) * beta[r] for c < r within the chunk; k bf16
+ * [T][H][128], g fp32 [T][HV], beta bf16 [T][HV], A bf16 [T][HV][64] (row r written up to the end of its 16-column
+ * block; other entries untouched). Computed in fp32 (the reference uses bf16 / tf32 tensor-core products and an
+ * approximate ex2: agreement with it is to that accuracy). Returns -1 for HV != 2H (the reference's code),
+ * hipErrorInvalidConfiguration for NT or H <= 0 (an empty grid), hipErrorInvalidValue for missing or misaligned
+ * buffers, else hipGetLastError(). */
+int reax_kkt(const void* k, const void* g, const void* beta, void* A, const void* cu, const void* cidx, int NT, int H,
+             int HV, void* stream);
+/* Bytes of LDS the reax_kkt kernel uses (the reference returns its shared-memory size, reax_kkt.cu:272). */
+int reax_kkt_smem(void);
 
 #ifdef __cplusplus
 }

@@ -16,6 +16,14 @@
 // The reference evaluates r with CUDA's approximate rsqrtf; this oracle (like the HIP kernel) evaluates it in
 // double precision and rounds to fp32: bit-exact agreement with the reference at that step is not claimed.
 //
+// oracle_kkt restates libreax_howu/reax_kkt.cu ("kkt" below; the Gated-DeltaNet chunk solve), in double precision:
+//   per chunk (sequence i_n, chunk i_t of 64 tokens; cidx pairs) and key head kh, for value heads hv = 2kh, 2kh+1:
+//   M[r][c] = (k_r . k_c) * 2^(g[r] - g[c]) * beta[r] for c < r < nval, else 0; g[r] - g[c] rounded to fp32 as the
+//   reference subtracts in fp32 before ex2 (kkt:134-140); A = (I + M)^-1 (the diagonal-block inverses by forward
+//   substitution and the block recurrence of kkt:170-240 compute exactly this lower-triangular inverse); rows r <
+//   nval, columns up to the end of the row's 16-column block, stored as bf16 (kkt:191-199, 243-258).
+// The reference's bf16 / tf32 tensor-core products and approximate ex2 make it agree with this to its own accuracy.
+//
 // oracle_conv restates libreax_howu/reax_conv_v2.cu ("conv" below; causal 4-tap conv1d + SiLU + L2 norm):
 //   tap j = 0..3: src = meta.x - 3 + j, skipped when src < 0; row meta.z + src of qkv when src >= meta.y, else row
 //   meta.w + src of the cache                                                                        (conv:88-92)
@@ -170,6 +178,66 @@ int oracle_conv(const uint16_t* qkv, long long SX, const uint16_t* cache, int C,
       } else if (!skip_v) {
         uint16_t* dst = v + (long long)t * VD + (128LL * u - 2 * KD);
         for (int c = 0; c < 128; ++c) dst[c] = f2bf(s[c]);
+      }
+    }
+  }
+  return 0;
+}
+
+// mutant != 0 plants a deliberate mistake (used only to show that the pinning tests catch it):
+//   1: decay 2^(g[c] - g[r]); 2: beta of the column; 3: the diagonal included in M; 4: the sign of the
+//   off-diagonal entries lost (x_r = +sum)
+int oracle_kkt(const uint16_t* k, const float* g, const uint16_t* beta, uint16_t* A, const int64_t* cu,
+               const int64_t* cidx, int NT, int H, int HV, int mutant) {
+  if (HV != 2 * H) return -1;
+  for (int ch = 0; ch < NT; ++ch) {
+    const int64_t i_n = cidx[2 * ch], i_t = cidx[2 * ch + 1];
+    const int64_t bos = cu[i_n];
+    const int T = (int)(cu[i_n + 1] - bos), t0 = (int)i_t * 64;
+    const int nval = T - t0 < 64 ? T - t0 : 64;
+    for (int kh = 0; kh < H; ++kh) {
+      double raw[64][64];
+      for (int r = 0; r < nval; ++r)
+        for (int c = 0; c <= r; ++c) {
+          double acc = 0.0;
+          for (int d = 0; d < 128; ++d)
+            acc += (double)bf2f(k[((bos + t0 + r) * H + kh) * 128 + d]) * (double)bf2f(k[((bos + t0 + c) * H + kh) * 128 + d]);
+          raw[r][c] = acc;
+        }
+      for (int v = 0; v < 2; ++v) {
+        const int hv = 2 * kh + v;
+        auto G = [&](int r) { return g[(bos + t0 + r) * HV + hv]; };
+        auto Bt = [&](int r) { return (double)bf2f(beta[(bos + t0 + r) * HV + hv]); };
+        static thread_local double M[64][64];
+        for (int r = 0; r < 64; ++r)
+          for (int c = 0; c < 64; ++c) {
+            M[r][c] = 0.0;
+            const bool in = mutant == 3 ? c <= r : c < r;
+            if (!in || r >= nval) continue;
+            const float dg = mutant == 1 ? G(c) - G(r) : G(r) - G(c);
+            M[r][c] = raw[r][c] * std::exp2((double)dg) * (mutant == 2 ? Bt(c) : Bt(r));
+          }
+        // X = (I + M)^-1, column by column
+        double X[64][64];
+        for (int j = 0; j < 64; ++j) {
+          for (int r = 0; r < 64; ++r) {
+            if (r < j) { X[r][j] = 0.0; continue; }
+            double s = 0.0;
+            for (int c = j; c < r; ++c) s += M[r][c] * X[c][j];
+            if (mutant == 3) {
+              X[r][j] = ((r == j ? 1.0 : 0.0) - s) / (1.0 + M[r][r]);
+            } else {
+              X[r][j] = r == j ? 1.0 : (mutant == 4 ? s : -s);
+            }
+          }
+        }
+        for (int r = 0; r < nval; ++r) {
+          const int cend = 16 * (r / 16 + 1);
+          for (int c = 0; c < cend; ++c) {
+            const float xf = (float)X[r][c];
+            A[((bos + t0 + r) * HV + hv) * 64 + c] = xf == 0.f ? 0 : f2bf(xf);
+          }
+        }
       }
     }
   }

@@ -260,3 +260,26 @@ def conv(qkv, SX, cache, C, meta, w, Tf, *, KD, VD, eps=1e-6, rep=1, skip_v=0, u
     L.oracle_conv(_ptr(qkv), SX, _ptr(cache), C, _ptr(meta), _ptr(w), _ptr(q), _ptr(k), _ptr(v), Tf,
                   ctypes.c_float(eps), KD, VD, rep, skip_v, u0, units, m, _ptr(rstd))
     return q, k, v, rstd
+
+
+KKT_MUTANTS = {"kkt_decay_sign": 1, "kkt_beta_column": 2, "kkt_diag_in_m": 3, "kkt_sign": 4}
+
+
+def kkt(k, g, beta, cu, cidx, *, NT, H, HV, A=None, mutant=0):
+    """reax_kkt on the CPU (double precision): k bf16 bits [T][H][128], g fp32 [T][HV], beta bf16 bits [T][HV],
+    cu / cidx int64. Writes into A (bf16 bits [T][HV][64], allocated zero-filled if None); returns (code, A)."""
+    L = gdn_lib()
+    if not hasattr(L, "_kkt_typed"):
+        L.oracle_kkt.restype = ctypes.c_int
+        L.oracle_kkt.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int] * 4
+        L._kkt_typed = True
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    beta = np.ascontiguousarray(beta, dtype=np.uint16)
+    cu = np.ascontiguousarray(cu, dtype=np.int64)
+    cidx = np.ascontiguousarray(cidx, dtype=np.int64)
+    if A is None:
+        A = np.zeros((k.shape[0], HV, 64), dtype=np.uint16)
+    m = KKT_MUTANTS.get(mutant, mutant) if isinstance(mutant, str) else mutant
+    code = L.oracle_kkt(_ptr(k), _ptr(g), _ptr(beta), _ptr(A), _ptr(cu), _ptr(cidx), NT, H, HV, m)
+    return code, A

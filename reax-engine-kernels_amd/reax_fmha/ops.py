@@ -188,3 +188,16 @@ def conv_v(qkv, cache, meta, w, *, Tf, KD, VD, v=None):
                                 w.data_ptr(), v.data_ptr(), Tf, KD, VD, _stream())
     _check("reax_conv_v", rc)
     return v
+
+
+def kkt(k, g, beta, cu, cidx, *, NT, H, HV, A=None):
+    """reax_kkt (libreax_howu/reax_kkt.cu:263-270) on device tensors: k bf16 [T][H][128], g fp32 [T][HV], beta bf16
+    [T][HV], cu / cidx int64. Writes A (bf16 [T][HV][64], allocated if None: entries outside the lower block
+    triangle stay as allocated) and returns it."""
+    _dev(k, g, beta, cu, cidx)
+    if A is None:
+        A = torch.zeros((k.shape[0], HV, 64), dtype=torch.bfloat16, device=k.device)
+    rc = abi.howu().reax_kkt(k.data_ptr(), g.data_ptr(), beta.data_ptr(), A.data_ptr(), cu.data_ptr(),
+                             cidx.data_ptr(), NT, H, HV, _stream())
+    _check("reax_kkt", rc)
+    return A

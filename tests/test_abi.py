@@ -58,9 +58,8 @@ def test_null_bias_returns_minus_one(loader):
 
 def test_gdn_entry_points_not_implemented():
     L = abi.howu()
-    assert L.howu3_smem() == 0 and L.reax_kkt_smem() == 0
+    assert L.howu3_smem() == 0
     assert L.reax_howu(*([None] * 8 + [1.0, 1, 1, 1, None])) == abi.REAX_ERR_NOT_IMPLEMENTED
-    assert L.reax_kkt(*([None] * 6 + [1, 1, 2, None])) == abi.REAX_ERR_NOT_IMPLEMENTED
 
 
 def test_rarn_argument_codes():
@@ -87,6 +86,16 @@ def test_conv_argument_codes():
     assert L.reax_conv_l2(*l2(4, 16)) == 1
     assert L.reax_conv_v(None, 0, None, 0, None, None, None, 0, 128, 128, None) == 0
     assert L.reax_conv_v(None, 0, None, 0, None, None, None, 3, 128, 128, None) == 1
+
+
+def test_kkt_argument_codes():
+    # reax_kkt: HV != 2H -> -1 (kkt:265); an empty grid -> hipErrorInvalidConfiguration (the reference's launch
+    # error); missing buffers -> hipErrorInvalidValue; none of these launches. reax_kkt_smem: the kernel's LDS bytes
+    L = abi.howu()
+    assert L.reax_kkt(*([None] * 6 + [1, 2, 3, None])) == -1
+    assert L.reax_kkt(*([None] * 6 + [0, 2, 4, None])) == 9
+    assert L.reax_kkt(*([None] * 6 + [3, 2, 4, None])) == 1
+    assert 0 < L.reax_kkt_smem() <= 160 * 1024
 
 
 def test_splitkv_workspace_size():
