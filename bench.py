@@ -9,6 +9,7 @@ pairs). A "step" is one attention forward over the resident inputs. Also reporte
   - "rarn": the reduce-add RMSNorm (reax_rarn) over 8192 rows of 2560 with 4 partials, HBM GB/s against 8 TB/s;
   - "conv": the causal conv + SiLU + L2 norm (reax_conv_l2, rep 2) over 4096 tokens, HBM GB/s against 8 TB/s;
   - "kkt": the GDN chunk solve (reax_kkt) over 8192 tokens x 16 key heads, GB/s of k read + A written;
+  - "howu": the GDN chunked forward (reax_howu) over 8 x 2048 tokens, 32 value heads, TFLOP/s of its chunk products;
   - "cpu_baseline": the OpenMP fp32 build of the CPU reference on a bounded sample of config 2's rows.
 Only N = 1 GPU is supported: the path is single-GPU by design.
 """
@@ -241,6 +242,45 @@ def bench_kkt(torch, ops, iters=20):
     return ms, nbytes / (ms * 1e-3) / 1e9
 
 
+HOWU_N, HOWU_T, HOWU_H = 8, 2048, 16  # GDN chunked-forward leg: 8 sequences of 2048 tokens, 16 key / 32 value heads
+
+
+def bench_howu(torch, ops, iters=10):
+    """reax_howu over HOWU_N sequences of HOWU_T tokens (one workgroup per sequence and value head); returns
+    (ms, TFLOP/s) with the FLOPs of the chunk products the reference performs per 64-token chunk and value head:
+    A vb, A kb (64x64x128 each), q k^T (64x64x128), w h, q h (64x128x128 each), AQ vn (64x64x128), k^T vdec
+    (128x64x128)."""
+    N, T, H = HOWU_N, HOWU_T, HOWU_H
+    HV = 2 * H
+    g_ = torch.Generator(device="cuda").manual_seed(6)
+    TT = N * T
+    nrm = lambda x: (x / x.norm(dim=-1, keepdim=True)).to(torch.bfloat16)
+    q = nrm(torch.randn((TT, H, 128), device="cuda", generator=g_))
+    k = nrm(torch.randn((TT, H, 128), device="cuda", generator=g_))
+    v = torch.randn((TT, HV, 128), device="cuda", generator=g_).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn((TT, HV), device="cuda", generator=g_)).to(torch.bfloat16)
+    d = -torch.rand((TT // 64, 64, HV), device="cuda", generator=g_) * 0.1
+    g = torch.cumsum(d, 1).reshape(TT, HV).float()
+    A = (torch.randn((TT, HV, 64), device="cuda", generator=g_) * 0.05).to(torch.bfloat16)
+    cu = torch.arange(0, (N + 1) * T, T, dtype=torch.int64, device="cuda")
+    o = torch.empty((TT, HV, 128), dtype=torch.bfloat16, device="cuda")
+    run = lambda: ops.howu(q, k, v, beta, A, g, cu, N=N, H=H, HV=HV, scale=128 ** -0.5, o=o)
+    run()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(iters):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        run()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    ms = float(np.median(ts))
+    flops_chunk = 2 * (3 * 64 * 64 * 128 + 2 * 64 * 128 * 128 + 64 * 64 * 128 + 128 * 64 * 128)
+    flops = flops_chunk * (TT // 64) * HV
+    return ms, flops / (ms * 1e-3) / 1e12
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -251,7 +291,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "rarn", "conv", "kkt"], help="run one leg only (for profiling)")
+    ap.add_argument("--only", choices=["prefill", "decode", "rarn", "conv", "kkt", "howu"], help="run one leg only (for profiling)")
     ap.add_argument("--no-gdn", action="store_true", help="skip the reax_rarn, reax_conv_l2 and reax_kkt legs")
     ap.add_argument("--decode-splits", type=int, default=0, help="override config 4's key-split count")
     ap.add_argument("--calib-copy", action="store_true",
@@ -276,6 +316,11 @@ def main():
 
     from reax_fmha import ops
 
+    if args.only == "howu":
+        ms, tf = bench_howu(torch, ops)
+        print(json.dumps({"howu_TFLOPs": round(tf, 2), "ms": round(ms, 4), "seqs": HOWU_N, "tokens": HOWU_T}),
+              flush=True)
+        return
     if args.only == "kkt":
         ms, gbs = bench_kkt(torch, ops)
         print(json.dumps({"kkt_GBs": round(gbs, 1), "ms": round(ms, 4), "tokens": KKT_T, "key_heads": KKT_H}),
@@ -343,6 +388,11 @@ def main():
                        "unit": "GB/s", "ms": round(ms, 4),
                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
                                     "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
+        ms, tf = bench_howu(torch, ops)
+        line["howu"] = {"workload": f"reax_howu {HOWU_N} x {HOWU_T} tokens, {HOWU_H} key / {2 * HOWU_H} value heads",
+                        "value": round(tf, 2), "unit": "TFLOP/s", "ms": round(ms, 4),
+                        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": W.BF16_PEAK_TFLOPS,
+                                     "unit": "TFLOP/s", "frac": round(tf / W.BF16_PEAK_TFLOPS, 4)}}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

@@ -24,6 +24,19 @@
 //   nval, columns up to the end of the row's 16-column block, stored as bf16 (kkt:191-199, 243-258).
 // The reference's bf16 / tf32 tensor-core products and approximate ex2 make it agree with this to its own accuracy.
 //
+// oracle_howu restates libreax_howu/reax_howu.cu ("howu" below; the Gated-DeltaNet chunked forward, skip-A form):
+//   per sequence and value head hv (key head hv / (HV/H)), state h [128 k][128 v] = 0; per 64-token chunk (g is the
+//   chunk-local cumulative log2 decay, eg = 2^g):
+//   vb = bf16(v beta); kb = bf16(bf16(k beta) eg)                                                  (howu:95-104, 146-156)
+//   u = A vb, w = A kb over the lower block triangle of A; ub = bf16(u), wb = bf16(w)              (howu:131-163, 202-208)
+//   AQ[t][s] = bf16((q_t . k_s) 2^(g_t - g_s)) for s <= t, both valid, else 0                        (howu:165-196)
+//   vw = wb bf16(h), oi = q bf16(h); x = ub - vw; vn = bf16(x); vdec = bf16(x 2^(g_last - g_t))      (howu:210-244)
+//   o = bf16(fma(AQ vn, scale, (oi 2^(g_t)) scale))                                                 (howu:256-283)
+//   h = h 2^(g_last) + k^T vdec                                                                     (howu:285-300)
+// Products are summed in double (the reference's tensor-core sums are fp32 in a hardware order). exact != 0 drops
+// every bf16 rounding and uses the exact (I + M)^-1 computed here instead of the given A: that form must equal the
+// token-by-token gated delta rule, which the tests check.
+//
 // oracle_conv restates libreax_howu/reax_conv_v2.cu ("conv" below; causal 4-tap conv1d + SiLU + L2 norm):
 //   tap j = 0..3: src = meta.x - 3 + j, skipped when src < 0; row meta.z + src of qkv when src >= meta.y, else row
 //   meta.w + src of the cache                                                                        (conv:88-92)
@@ -40,6 +53,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <vector>
 
 namespace {
 
@@ -112,6 +126,119 @@ int oracle_rarn(const uint16_t* part, int S, int serial, long long pstride, cons
       const float wv = bf2f(w[c]);
       const float g = mutant == 2 ? wv : 1.f + wv;
       out[ro + c] = f2bf((hrow[c] * r) * g);
+    }
+  }
+  return 0;
+}
+
+// mutant != 0 plants a deliberate mistake (used only to show that the pinning tests catch it):
+//   1: the inter-chunk output term without its 2^(g_t) decay; 2: the intra-chunk causal mask strict (s < t);
+//   3: the state carried without its chunk decay 2^(g_last); 4: vdec without the 2^(g_last - g_t) factor
+int oracle_howu(const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* beta, const uint16_t* A,
+                const float* g, uint16_t* o, const int64_t* cu, float scale, int N, int H, int HV, int exact,
+                int mutant) {
+  if (H <= 0 || HV % H) return -1;
+  const int rep = HV / H;
+  auto rb = [&](double x) -> double { return exact ? x : (double)bf2f(f2bf((float)x)); };
+  std::vector<double> h(128 * 128), Hs(128 * 128);
+  std::vector<double> Ac(64 * 64), vb(64 * 128), kb(64 * 128), ub(64 * 128), wb(64 * 128), AQ(64 * 64);
+  std::vector<double> vn(64 * 128), vdec(64 * 128), qf(64 * 128), kf(64 * 128);
+  for (int i_n = 0; i_n < N; ++i_n) {
+    const int64_t bos = cu[i_n];
+    const int T = (int)(cu[i_n + 1] - bos);
+    for (int hv = 0; hv < HV; ++hv) {
+      const int kh = hv / rep;
+      std::fill(h.begin(), h.end(), 0.0);
+      for (int t0 = 0; t0 < T; t0 += 64) {
+        const int nv = T - t0 < 64 ? T - t0 : 64;
+        double G[64], eg[64], Bt[64];
+        for (int t = 0; t < 64; ++t) {
+          G[t] = t < nv ? (double)g[(bos + t0 + t) * HV + hv] : 0.0;
+          eg[t] = std::exp2(G[t]);
+          Bt[t] = t < nv ? (double)bf2f(beta[(bos + t0 + t) * HV + hv]) : 0.0;
+        }
+        for (int t = 0; t < 64; ++t)
+          for (int d = 0; d < 128; ++d) {
+            qf[t * 128 + d] = t < nv ? (double)bf2f(q[((bos + t0 + t) * H + kh) * 128 + d]) : 0.0;
+            kf[t * 128 + d] = t < nv ? (double)bf2f(k[((bos + t0 + t) * H + kh) * 128 + d]) : 0.0;
+            const double vv = t < nv ? (double)bf2f(v[((bos + t0 + t) * HV + hv) * 128 + d]) : 0.0;
+            vb[t * 128 + d] = rb(vv * Bt[t]);
+            kb[t * 128 + d] = rb(rb(kf[t * 128 + d] * Bt[t]) * eg[t]);
+          }
+        // A: the given bf16 lower block triangle (upper blocks read as 0), or the exact inverse
+        if (exact) {
+          double M[64][64];
+          for (int r = 0; r < 64; ++r)
+            for (int c = 0; c < 64; ++c) {
+              M[r][c] = 0.0;
+              if (c < r && r < nv) {
+                double dot = 0.0;
+                for (int d = 0; d < 128; ++d) dot += kf[r * 128 + d] * kf[c * 128 + d];
+                M[r][c] = dot * std::exp2(G[r] - G[c]) * Bt[r];
+              }
+            }
+          for (int j = 0; j < 64; ++j)
+            for (int r = 0; r < 64; ++r) {
+              if (r < j) { Ac[r * 64 + j] = 0.0; continue; }
+              double sacc = 0.0;
+              for (int c = j; c < r; ++c) sacc += M[r][c] * Ac[c * 64 + j];
+              Ac[r * 64 + j] = r == j ? 1.0 : -sacc;
+            }
+        } else {
+          for (int r = 0; r < 64; ++r)
+            for (int c = 0; c < 64; ++c)
+              Ac[r * 64 + c] = (r < nv && c / 16 <= r / 16) ? (double)bf2f(A[((bos + t0 + r) * HV + hv) * 64 + c]) : 0.0;
+        }
+        for (int t = 0; t < 64; ++t)
+          for (int c = 0; c < 128; ++c) {
+            double su = 0.0, sw = 0.0;
+            for (int s2 = 0; s2 < 64; ++s2) {
+              su += Ac[t * 64 + s2] * vb[s2 * 128 + c];
+              sw += Ac[t * 64 + s2] * kb[s2 * 128 + c];
+            }
+            ub[t * 128 + c] = rb(su);
+            wb[t * 128 + c] = rb(sw);
+          }
+        for (int t = 0; t < 64; ++t)
+          for (int s2 = 0; s2 < 64; ++s2) {
+            double z = 0.0;
+            const bool in = mutant == 2 ? s2 < t : s2 <= t;
+            if (in && t < nv && s2 < nv) {
+              double dot = 0.0;
+              for (int d = 0; d < 128; ++d) dot += qf[t * 128 + d] * kf[s2 * 128 + d];
+              z = rb(dot * std::exp2((double)((float)G[t] - (float)G[s2])));
+            }
+            AQ[t * 64 + s2] = z;
+          }
+        for (int i = 0; i < 128 * 128; ++i) Hs[i] = rb(h[i]);
+        const double glast = G[nv - 1];
+        for (int t = 0; t < 64; ++t) {
+          const double da = t < nv ? (mutant == 4 ? 1.0 : std::exp2(glast - G[t])) : 0.0;
+          for (int c = 0; c < 128; ++c) {
+            double vw = 0.0;
+            for (int d = 0; d < 128; ++d) vw += wb[t * 128 + d] * Hs[d * 128 + c];
+            const double x = ub[t * 128 + c] - vw;
+            vn[t * 128 + c] = rb(x);
+            vdec[t * 128 + c] = rb(x * da);
+          }
+        }
+        for (int t = 0; t < nv; ++t)
+          for (int c = 0; c < 128; ++c) {
+            double oi = 0.0, ci = 0.0;
+            for (int d = 0; d < 128; ++d) oi += qf[t * 128 + d] * Hs[d * 128 + c];
+            for (int s2 = 0; s2 < 64; ++s2) ci += AQ[t * 64 + s2] * vn[s2 * 128 + c];
+            const double inter = (mutant == 1 ? oi : oi * eg[t]) * scale;
+            const double r = ci * scale + inter;
+            o[((bos + t0 + t) * HV + hv) * 128 + c] = exact ? f2bf((float)r) : f2bf((float)r);
+          }
+        const double dl = mutant == 3 ? 1.0 : std::exp2(glast);
+        for (int d = 0; d < 128; ++d)
+          for (int c = 0; c < 128; ++c) {
+            double acc = h[d * 128 + c] * dl;
+            for (int t = 0; t < 64; ++t) acc += kf[t * 128 + d] * vdec[t * 128 + c];
+            h[d * 128 + c] = acc;
+          }
+      }
     }
   }
   return 0;

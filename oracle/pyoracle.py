@@ -283,3 +283,29 @@ def kkt(k, g, beta, cu, cidx, *, NT, H, HV, A=None, mutant=0):
     m = KKT_MUTANTS.get(mutant, mutant) if isinstance(mutant, str) else mutant
     code = L.oracle_kkt(_ptr(k), _ptr(g), _ptr(beta), _ptr(A), _ptr(cu), _ptr(cidx), NT, H, HV, m)
     return code, A
+
+
+HOWU_MUTANTS = {"howu_inter_no_decay": 1, "howu_strict_causal": 2, "howu_state_no_decay": 3, "howu_vdec_no_decay": 4}
+
+
+def howu(q, k, v, beta, A, g, cu, *, N, H, HV, scale, exact=False, o=None, mutant=0):
+    """reax_howu on the CPU: q, k bf16 bits [T][H][128], v bf16 [T][HV][128], beta bf16 [T][HV], A bf16 [T][HV][64]
+    (ignored when exact), g fp32 [T][HV] (chunk-local cumulative log2 decay), cu int64. Returns o, bf16 bits
+    [T][HV][128] (rows written for every token)."""
+    L = gdn_lib()
+    if not hasattr(L, "_howu_typed"):
+        L.oracle_howu.restype = ctypes.c_int
+        L.oracle_howu.argtypes = [ctypes.c_void_p] * 8 + [ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                          ctypes.c_int, ctypes.c_int]
+        L._howu_typed = True
+    arrs = [np.ascontiguousarray(x, dtype=np.uint16) for x in (q, k, v, beta)]
+    A = np.ascontiguousarray(A if A is not None else np.zeros((q.shape[0], HV, 64)), dtype=np.uint16)
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    cu = np.ascontiguousarray(cu, dtype=np.int64)
+    if o is None:
+        o = np.zeros((q.shape[0], HV, 128), dtype=np.uint16)
+    m = HOWU_MUTANTS.get(mutant, mutant) if isinstance(mutant, str) else mutant
+    code = L.oracle_howu(_ptr(arrs[0]), _ptr(arrs[1]), _ptr(arrs[2]), _ptr(arrs[3]), _ptr(A), _ptr(g), _ptr(o),
+                         _ptr(cu), ctypes.c_float(scale), N, H, HV, int(exact), m)
+    assert code == 0, code
+    return o

@@ -201,3 +201,17 @@ def kkt(k, g, beta, cu, cidx, *, NT, H, HV, A=None):
                              cidx.data_ptr(), NT, H, HV, _stream())
     _check("reax_kkt", rc)
     return A
+
+
+def howu(q, k, v, beta, A, g, cu, *, N, H, HV, scale, o=None, dense=False):
+    """reax_howu (skip form) or howu3_dense (libreax_howu/reax_howu.cu:349-376) on device tensors: q, k bf16
+    [T][H][128], v bf16 [T][HV][128], beta bf16 [T][HV], A bf16 [T][HV][64] (the chunk solve's output), g fp32
+    [T][HV] (chunk-local cumulative log2 decay), cu int64 [N+1]. Returns o, bf16 [T][HV][128]."""
+    _dev(q, k, v, beta, A, g, cu)
+    if o is None:
+        o = torch.empty((q.shape[0], HV, 128), dtype=torch.bfloat16, device=q.device)
+    fn = abi.howu().howu3_dense if dense else abi.howu().reax_howu
+    rc = fn(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), A.data_ptr(), g.data_ptr(), o.data_ptr(),
+            cu.data_ptr(), scale, N, H, HV, _stream())
+    _check("reax_howu", rc)
+    return o

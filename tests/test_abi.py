@@ -58,8 +58,8 @@ def test_null_bias_returns_minus_one(loader):
 
 def test_gdn_entry_points_not_implemented():
     L = abi.howu()
-    assert L.howu3_smem() == 0
-    assert L.reax_howu(*([None] * 8 + [1.0, 1, 1, 1, None])) == abi.REAX_ERR_NOT_IMPLEMENTED
+    assert L.reax_howu_norm(*([None] * 8 + [1.0, 1, 1, 2, None, None, None, 0, None, 1e-6, 1.0])) == \
+        abi.REAX_ERR_NOT_IMPLEMENTED
 
 
 def test_rarn_argument_codes():
@@ -96,6 +96,17 @@ def test_kkt_argument_codes():
     assert L.reax_kkt(*([None] * 6 + [0, 2, 4, None])) == 9
     assert L.reax_kkt(*([None] * 6 + [3, 2, 4, None])) == 1
     assert 0 < L.reax_kkt_smem() <= 160 * 1024
+
+
+def test_howu_argument_codes():
+    # reax_howu / howu3_skip / howu3_dense: an empty grid -> hipErrorInvalidConfiguration (the reference's launch
+    # error); H not dividing HV or missing buffers -> hipErrorInvalidValue; howu3_smem: the kernel's LDS bytes
+    L = abi.howu()
+    for fn in (L.reax_howu, L.howu3_skip, L.howu3_dense):
+        assert fn(*([None] * 8 + [1.0, 0, 1, 2, None])) == 9
+        assert fn(*([None] * 8 + [1.0, 1, 3, 2, None])) == 1
+        assert fn(*([None] * 8 + [1.0, 1, 1, 2, None])) == 1
+    assert 0 < L.howu3_smem() <= 160 * 1024
 
 
 def test_splitkv_workspace_size():
