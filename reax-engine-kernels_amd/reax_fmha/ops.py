@@ -215,3 +215,15 @@ def howu(q, k, v, beta, A, g, cu, *, N, H, HV, scale, o=None, dense=False):
             cu.data_ptr(), scale, N, H, HV, _stream())
     _check("reax_howu", rc)
     return o
+
+
+def howu_norm(q, k, v, beta, A, g, cu, f2s, z, nw, *, N, H, HV, scale, eps, factor, out):
+    """reax_howu_norm (libreax_howu/reax_howu_norm_v3.cu:431-435): the chunked forward with the fused gated-RMSNorm
+    epilogue; token t writes row f2s[t] of out (bf16 [rows][HV][128]); z: gate bf16 [rows][HV*128] (row stride
+    z.stride(0)); nw: norm weight bf16 [128]. Returns out."""
+    _dev(q, k, v, beta, A, g, cu, f2s, z, nw, out)
+    rc = abi.howu().reax_howu_norm(q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), A.data_ptr(),
+                                   g.data_ptr(), out.data_ptr(), cu.data_ptr(), scale, N, H, HV, _stream(),
+                                   f2s.data_ptr(), z.data_ptr(), z.stride(0), nw.data_ptr(), eps, factor)
+    _check("reax_howu_norm", rc)
+    return out

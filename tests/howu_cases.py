@@ -116,3 +116,66 @@ def pin_rows(mutant=0):
 
 
 ALL_PINS = [pin_recurrence, pin_faithful, pin_rows]
+
+
+# ------------------------------------------------------------------------------ gated-norm epilogue (reax_howu_norm)
+
+def make_norm_inputs(a, seed, *, drop=0.2):
+    """f2s (token -> output row, some tokens -1), gate z [rows][HV][128] bf16 (row stride HV*128), norm weight [128]."""
+    rng = np.random.default_rng(seed)
+    T, HV = a["T"], a["HV"]
+    rows = rng.permutation(T).astype(np.int32)
+    rows[rng.random(T) < drop] = -1
+    z = f32_to_bf16((rng.standard_normal((T, HV, 128)) * 2.0).astype(np.float32))
+    nw = f32_to_bf16((1.0 + 0.1 * rng.standard_normal(128)).astype(np.float32))
+    return dict(f2s=rows, z=z, ZS=HV * 128, nw=nw, eps=1e-6, factor=1.0 / 128)
+
+
+def norm_epilogue(o_bits, a, n):
+    """The gated-RMSNorm epilogue of reax_howu_norm (norm_v3:347-392) on the chunked forward's bf16 o, in numpy
+    float32 with its rounding points: out [T][HV][128] bf16 bits, rows not addressed left at SENT."""
+    T, HV = a["T"], a["HV"]
+    f = np.float32
+    out = np.full((T, HV, 128), SENT, np.uint16)
+    x = bf16_to_f32(o_bits)                                   # [T][HV][128]
+    sq = (x * x).astype(f).reshape(T, HV, 32, 4)
+    p = (((sq[..., 0] + sq[..., 1]).astype(f) + sq[..., 2]).astype(f) + sq[..., 3]).astype(f)  # [T][HV][32]
+    for d in (16, 8, 4, 2, 1):
+        p = p.copy()
+        p[..., :d] = (p[..., :d] + p[..., d:2 * d]).astype(f)
+    tot = p[..., 0]
+    rr = (1.0 / np.sqrt(((tot * f(n["factor"])).astype(f) + f(n["eps"])).astype(f).astype(np.float64))).astype(f)
+    y = bf16_to_f32(f32_to_bf16((x * rr[..., None]).astype(f)))
+    w = bf16_to_f32(n["nw"])
+    y2 = bf16_to_f32(f32_to_bf16((w[None, None, :] * y).astype(f)))
+    for t in range(T):
+        R = n["f2s"][t]
+        if R < 0:
+            continue
+        zz = bf16_to_f32(n["z"][R]).astype(np.float64)
+        d1 = (1.0 + np.exp(-zz)).astype(f)
+        sz = (bf16_to_f32(n["z"][R]) / d1).astype(f)
+        out[R] = f32_to_bf16((y2[t] * sz).astype(f))
+    return out
+
+
+def pin_norm_formula(mutant=0):
+    """The epilogue against the float64 gated RMSNorm y = w * o / sqrt(mean(o^2) + eps) * silu(z) to 2 bf16 ulps
+    (the factor 1/128 makes sum * factor the mean)."""
+    a = make_inputs([70, 30], 1, 2, 9)
+    o = run(a, A=chunk_solve(a), mutant=mutant)
+    n = make_norm_inputs(a, 10)
+    out = norm_epilogue(o, a, n)
+    x = bf16_to_f32(o).astype(np.float64)
+    w = bf16_to_f32(n["nw"]).astype(np.float64)
+    for t in range(a["T"]):
+        R = n["f2s"][t]
+        if R < 0:
+            continue
+        zz = bf16_to_f32(n["z"][R]).astype(np.float64)
+        want = w * x[t] / np.sqrt((x[t] ** 2).mean(axis=1, keepdims=True) + n["eps"]) * (zz / (1 + np.exp(-zz)))
+        got = bf16_to_f32(out[R]).astype(np.float64)
+        assert np.all(np.abs(got - want) <= np.abs(want) * 2.0 ** -6 + 1e-6), f"norm epilogue off at token {t}"
+
+
+ALL_PINS.append(pin_norm_formula)

@@ -56,12 +56,6 @@ def test_null_bias_returns_minus_one(loader):
     assert L.reax_fmha_b(*args) == -1  # v8:439: returns before any launch
 
 
-def test_gdn_entry_points_not_implemented():
-    L = abi.howu()
-    assert L.reax_howu_norm(*([None] * 8 + [1.0, 1, 1, 2, None, None, None, 0, None, 1e-6, 1.0])) == \
-        abi.REAX_ERR_NOT_IMPLEMENTED
-
-
 def test_rarn_argument_codes():
     # reax_rarn (rarn_final.cu:100, 104): n <= 0 -> 0 (even with a wrong D), D != 2560 -> -1, S outside 2..8 -> -2;
     # a missing buffer (which the reference would fault on) -> hipErrorInvalidValue; none of these launches
@@ -107,6 +101,10 @@ def test_howu_argument_codes():
         assert fn(*([None] * 8 + [1.0, 1, 3, 2, None])) == 1
         assert fn(*([None] * 8 + [1.0, 1, 1, 2, None])) == 1
     assert 0 < L.howu3_smem() <= 160 * 1024
+    norm = lambda N, H, HV: [None] * 6 + [None, None, 1.0, N, H, HV, None, None, None, 0, None, 1e-6, 1.0]
+    assert L.reax_howu_norm(*norm(0, 1, 2)) == 9
+    assert L.reax_howu_norm(*norm(1, 3, 2)) == 1
+    assert L.reax_howu_norm(*norm(1, 1, 2)) == 1
 
 
 def test_splitkv_workspace_size():

@@ -56,6 +56,35 @@ def test_howu_matches_oracle(lens, H, HV, dense, seed):
     assert err.mean() <= scale * 2.0 ** -10, f"mean error {err.mean() / scale:.3g} of the output scale"
 
 
+@pytest.mark.parametrize("lens,H,HV,seed", [([70, 130], 1, 2, 30), ([5, 64, 100], 2, 4, 31)])
+def test_howu_norm_matches_oracle(lens, H, HV, seed):
+    """reax_howu_norm: the gated-RMSNorm epilogue rows (through f2s, some tokens dropped) against the epilogue of
+    the oracle's o, same tolerance; rows no token addresses stay untouched."""
+    from reax_fmha import ops
+
+    a = HC.make_inputs(lens, H, HV, seed)
+    n = HC.make_norm_inputs(a, seed + 100)
+    _say(f"norm lens={lens} H={H} HV={HV}")
+    A = HC.chunk_solve(a)
+    ref = HC.norm_epilogue(HC.run(a, A=A), a, n)
+    d = lambda x: W.bits_to_torch(x, "cuda")
+    out = d(np.full((a["T"], HV, 128), HC.SENT, np.uint16))
+    ops.howu_norm(d(a["q"]), d(a["k"]), d(a["v"]), d(a["beta"]), d(A), torch.from_numpy(a["g"]).cuda(),
+                  torch.from_numpy(a["cu"]).cuda(), torch.from_numpy(n["f2s"]).cuda(),
+                  d(n["z"]).reshape(a["T"], HV * 128), d(n["nw"]), N=len(lens), H=H, HV=HV, scale=a["scale"],
+                  eps=n["eps"], factor=n["factor"], out=out)
+    torch.cuda.synchronize()
+    ob = W.torch_to_bits(out).reshape(a["T"], HV, 128)
+    written = ref != HC.SENT
+    assert (ob[~written] == HC.SENT).all(), "wrote a row no token addresses"
+    got, want = bf16_to_f32(ob[written]).astype(np.float64), bf16_to_f32(ref[written]).astype(np.float64)
+    scale = np.abs(want).max()
+    err = np.abs(got - want)
+    _say(f"max err {err.max() / scale:.3g}, mean err {err.mean() / scale:.3g} of the output scale {scale:.3g}")
+    assert err.max() <= scale * 2.0 ** -6, f"max error {err.max() / scale:.3g} of the output scale"
+    assert err.mean() <= scale * 2.0 ** -10, f"mean error {err.mean() / scale:.3g} of the output scale"
+
+
 def test_howu_return_codes():
     from reax_fmha import abi
 
