@@ -9,11 +9,9 @@
  *   1. the reference's FMHA entry points (drop-in, head_dim 256);
  *   2. extension entry points for what the reference ABI cannot express (head_dim 128, LSE output, two-stride
  *      [S][Hq][D] row addressing, packed varlen sequences, split-KV decode with an LSE combine);
- *   3. the reference's Gated-DeltaNet chunk entry points, exported so that a loader which resolves every
- *      symbol still loads this library. They are not implemented yet: each returns REAX_ERR_NOT_IMPLEMENTED
- *      (the *_smem queries return 0) and launches nothing;
- *   4. the reference's reduce-add RMSNorm (reax_rarn), causal conv + SiLU + L2 norm (reax_conv_l2, reax_conv_v)
- *      and Gated-DeltaNet chunk solve (reax_kkt, reax_kkt_smem).
+ *   3. the reference's other kernels of this library: reduce-add RMSNorm (reax_rarn), causal conv + SiLU + L2 norm
+ *      (reax_conv_l2, reax_conv_v), Gated-DeltaNet chunk solve (reax_kkt, reax_kkt_smem) and chunked forward
+ *      (reax_howu, howu3_skip, howu3_dense, howu3_smem, reax_howu_norm).
  */
 #ifndef LIBREAX_HOWU_H
 #define LIBREAX_HOWU_H
@@ -24,8 +22,6 @@
 extern "C" {
 #endif
 
-/* hipErrorNotSupported: returned by the entry points whose kernels are not part of this library. */
-#define REAX_ERR_NOT_IMPLEMENTED 801
 
 /* ---- 1. reference FMHA entry points ------------------------------------------------------------------- */
 
@@ -79,24 +75,7 @@ int reax_fmha_splitkv(const void* q, const void* k, const void* v, const int* qp
                       long long osH, long long osT, long long osG, long long lsB, long long lsH, long long lsT,
                       long long lsG, void* stream);
 
-/* ---- 3. reference symbols outside the FMHA path (not implemented: return REAX_ERR_NOT_IMPLEMENTED) ------ */
-
-/* libreax_howu/reax_howu.cu:363-366 */
-int howu3_dense(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g, void* o,
-                const void* cu, float scale, int N, int H, int HV, void* stream);
-/* libreax_howu/reax_howu.cu:367-370 */
-int howu3_skip(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g, void* o,
-               const void* cu, float scale, int N, int H, int HV, void* stream);
-/* libreax_howu/reax_howu.cu:371 (returns 0 here: no kernel, no shared memory) */
-int howu3_smem(void);
-/* libreax_howu/reax_howu.cu:373-376 */
-int reax_howu(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g, void* o,
-              const void* cu, float scale, int N, int H, int HV, void* stream);
-/* libreax_howu/reax_howu_norm_v3.cu:431-435 */
-int reax_howu_norm(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g,
-                   void* out, const void* cu, float scale, int N, int H, int HV, void* stream, const void* f2s,
-                   const void* z, long long ZS, const void* nw, float eps, float factor);
-/* ---- 4. reference GDN-side entry points implemented here ------------------------------------------------ */
+/* ---- 3. the reference's Gated-DeltaNet / norm / conv entry points ------------------------------------------ */
 
 /* Reduce-add RMSNorm. Replaces reax_rarn, libreax_howu/reax_rarn_final.cu:98-106. Rows of D = 2560 bf16:
  * h = bf16(res + bf16(part[0] + ... + part[S-1])) (serial != 0: rounded to bf16 after every add), written to h_out;
@@ -137,6 +116,34 @@ int reax_kkt(const void* k, const void* g, const void* beta, void* A, const void
              int HV, void* stream);
 /* Bytes of LDS the reax_kkt kernel uses (the reference returns its shared-memory size, reax_kkt.cu:272). */
 int reax_kkt_smem(void);
+
+/* Gated-DeltaNet chunked forward (skip form: blocks of A above the diagonal 16 x 16 blocks read as 0). Replaces
+ * reax_howu, libreax_howu/reax_howu.cu:373-376. Per sequence (cu: int64 starts, N sequences) and value head hv (key
+ * head hv / (HV/H)): the gated delta rule over 64-token chunks with the reference's bf16 rounding points. q, k bf16
+ * [T][H][128]; v bf16 [T][HV][128]; beta bf16 [T][HV]; A bf16 [T][HV][64] (reax_kkt's output); g fp32 [T][HV] (the
+ * chunk-local cumulative log2 decay); o bf16 [T][HV][128]. The products accumulate in fp32 on the matrix cores:
+ * results agree with the reference's to bf16 accuracy. Returns hipErrorInvalidConfiguration for N or HV <= 0 (an
+ * empty grid), hipErrorInvalidValue when H does not divide HV or a buffer is missing / misaligned, else
+ * hipGetLastError(). */
+int reax_howu(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g, void* o,
+              const void* cu, float scale, int N, int H, int HV, void* stream);
+/* The same (reax_howu.cu:367-370). */
+int howu3_skip(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g, void* o,
+               const void* cu, float scale, int N, int H, int HV, void* stream);
+/* The dense form: every block of A is read (reax_howu.cu:363-366). */
+int howu3_dense(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g, void* o,
+                const void* cu, float scale, int N, int H, int HV, void* stream);
+/* Bytes of LDS the chunked-forward kernel uses (the reference returns its shared-memory size, reax_howu.cu:371). */
+int howu3_smem(void);
+/* The chunked forward with the fused gated-RMSNorm epilogue. Replaces reax_howu_norm,
+ * libreax_howu/reax_howu_norm_v3.cu:431-435: o is not stored; token t with R = f2s[t] >= 0 writes
+ * out[R][hv][c] = bf16(bf16(nw[c] bf16(o[c] rr)) silu(z[R * ZS + hv * 128 + c])), rr = 1/sqrt(sum(o^2) factor + eps)
+ * over the head's 128 values in the reference's order. rr and the SiLU exp are evaluated to fp32 accuracy where the
+ * reference uses rsqrtf and expf. Return codes as reax_howu; also hipErrorInvalidValue for a missing or misaligned
+ * f2s, z (8 bytes, ZS a multiple of 4) or nw. */
+int reax_howu_norm(const void* q, const void* k, const void* v, const void* beta, const void* A, const void* g,
+                   void* out, const void* cu, float scale, int N, int H, int HV, void* stream, const void* f2s,
+                   const void* z, long long ZS, const void* nw, float eps, float factor);
 
 #ifdef __cplusplus
 }

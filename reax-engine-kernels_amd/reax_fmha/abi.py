@@ -47,7 +47,6 @@ HOWU_SYMBOLS = ["reax_fmha_b", "reax_fmha_q", "reax_fmha_qx", "reax_fmha_varlen"
                 "reax_kkt_smem", "reax_rarn", "reax_howu_norm", "reax_conv_l2", "reax_conv_v"]
 POST_SYMBOLS = ["reax_fmha_b", "reax_fmha_q", "reax_fmha_qp"]
 
-REAX_ERR_NOT_IMPLEMENTED = 801
 
 _cache: dict[str, ctypes.CDLL] = {}
 
