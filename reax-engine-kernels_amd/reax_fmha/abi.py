@@ -39,13 +39,30 @@ SIGNATURES = {
     "reax_howu_norm": [P, P, P, P, P, P, P, P, F, I, I, I, P, P, P, LL, P, F, F],
     "reax_conv_l2": [P, LL, P, I, P, P, P, P, P, I, F, I, I, I, I, I, P],
     "reax_conv_v": [P, LL, P, I, P, P, P, I, I, I, P],
+    # the GEMM libraries (libreax_plain.so, libreax_slices.so, libreax_gv.so)
+    "reax_gemm_ncfg": [],
+    "reax_gemm_cfgname": [I],
+    "reax_gemm": [I, P, P, P, I, I, I, I, P],
+    "reax_slices_ncfg": [],
+    "reax_slices_cfgname": [I],
+    "reax_slices": [I, I, P, P, P, I, I, I, I, I, P],
+    "reax_gv_ncfg": [],
+    "reax_gv_cfgname": [I],
+    "reax_gv": [I, P, P, P, I, I, I, P],
 }
-RESTYPES = {"reax_fmha_splitkv_workspace": SZ}
+RESTYPES = {"reax_fmha_splitkv_workspace": SZ, "reax_gemm_cfgname": ctypes.c_char_p,
+            "reax_slices_cfgname": ctypes.c_char_p, "reax_gv_cfgname": ctypes.c_char_p}
 
 HOWU_SYMBOLS = ["reax_fmha_b", "reax_fmha_q", "reax_fmha_qx", "reax_fmha_varlen", "reax_fmha_splitkv_workspace",
                 "reax_fmha_splitkv", "howu3_dense", "howu3_skip", "howu3_smem", "reax_howu", "reax_kkt",
                 "reax_kkt_smem", "reax_rarn", "reax_howu_norm", "reax_conv_l2", "reax_conv_v"]
 POST_SYMBOLS = ["reax_fmha_b", "reax_fmha_q", "reax_fmha_qp"]
+PLAIN_SYMBOLS = ["reax_gemm_ncfg", "reax_gemm_cfgname", "reax_gemm"]
+SLICES_SYMBOLS = ["reax_slices_ncfg", "reax_slices_cfgname", "reax_slices"]
+GV_SYMBOLS = ["reax_gv_ncfg", "reax_gv_cfgname", "reax_gv"]
+PLAIN_PATH = os.path.join(LIB_DIR, "libreax_plain.so")
+SLICES_PATH = os.path.join(LIB_DIR, "libreax_slices.so")
+GV_PATH = os.path.join(LIB_DIR, "libreax_gv.so")
 
 
 _cache: dict[str, ctypes.CDLL] = {}
@@ -73,3 +90,18 @@ def howu() -> ctypes.CDLL:
 def post() -> ctypes.CDLL:
     """libreax_fmha_post.so with its three entry points typed."""
     return _load(POST_PATH, POST_SYMBOLS)
+
+
+def plain() -> ctypes.CDLL:
+    """libreax_plain.so (reax_gemm)."""
+    return _load(PLAIN_PATH, PLAIN_SYMBOLS)
+
+
+def slices() -> ctypes.CDLL:
+    """libreax_slices.so (reax_slices)."""
+    return _load(SLICES_PATH, SLICES_SYMBOLS)
+
+
+def gv() -> ctypes.CDLL:
+    """libreax_gv.so (reax_gv)."""
+    return _load(GV_PATH, GV_SYMBOLS)

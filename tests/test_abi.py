@@ -107,6 +107,38 @@ def test_howu_argument_codes():
     assert L.reax_howu_norm(*norm(1, 1, 2)) == 1
 
 
+@pytest.mark.parametrize("loader,symbols,path", [("plain", "PLAIN_SYMBOLS", "PLAIN_PATH"),
+                                                  ("slices", "SLICES_SYMBOLS", "SLICES_PATH"),
+                                                  ("gv", "GV_SYMBOLS", "GV_PATH")])
+def test_gemm_libraries_export_and_no_soname(loader, symbols, path):
+    # reference: libreax_plain.so / libreax_slices.so / libreax_gv.so export exactly their ncfg / cfgname / run
+    # symbols (gemm_plain2.cu:31-37, gemm_slices_v2.cu:55-65, gateup_vis2.cu:172-182), no soname
+    getattr(abi, loader)()
+    out = subprocess.run(["nm", "-D", "--defined-only", getattr(abi, path)], check=True, capture_output=True,
+                         text=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if " T " in ln}
+    assert exported == set(getattr(abi, symbols))
+    dyn = subprocess.run(["readelf", "-d", getattr(abi, path)], check=True, capture_output=True, text=True).stdout
+    assert "SONAME" not in dyn
+
+
+def test_gemm_argument_codes():
+    # config counts and names; an unknown cfg -> 9; shapes the reference's kernels cannot take -> 1 (plain, slices:
+    # CUTLASS can_implement; gv: K % 8 or N2 % 4, gv:143) or 3 (gv: an empty grid fails to launch); none launches
+    P, S, G = abi.plain(), abi.slices(), abi.gv()
+    assert (P.reax_gemm_ncfg(), S.reax_slices_ncfg(), G.reax_gv_ncfg()) == (15, 16, 20)
+    assert P.reax_gemm_cfgname(15) == b"?" and S.reax_slices_cfgname(-1) == b"?" and G.reax_gv_cfgname(20) == b"?"
+    assert P.reax_gemm_cfgname(0) != b"?" and S.reax_slices_cfgname(15) != b"?" and G.reax_gv_cfgname(19) != b"?"
+    assert P.reax_gemm(15, None, None, None, 8, 8, 8, 8, None) == 9
+    assert P.reax_gemm(0, None, None, None, 8, 8, 8, 8, None) == 1          # missing buffers
+    assert S.reax_slices(16, 1, None, None, None, 8, 8, 8, 1, 8, None) == 9
+    assert S.reax_slices(0, 1, None, None, None, 8, 8, 8, 2, 8, None) == 1  # S * kps > K
+    assert G.reax_gv(20, None, None, None, 8, 8, 8, None) == 9
+    assert G.reax_gv(0, None, None, None, 8, 8, 12, None) == 1              # K % 8
+    assert G.reax_gv(0, None, None, None, 8, 6, 8, None) == 1               # N2 % 4
+    assert G.reax_gv(0, None, None, None, 0, 8, 8, None) == 3               # empty grid
+
+
 def test_splitkv_workspace_size():
     L = abi.howu()
     # config 4: B 16, Hkv 8, M = G = 4 rows, D 128, 16 splits: partial O fp32 + LSE fp32, each 256-byte aligned
