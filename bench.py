@@ -10,6 +10,10 @@ pairs). A "step" is one attention forward over the resident inputs. Also reporte
   - "conv": the causal conv + SiLU + L2 norm (reax_conv_l2, rep 2) over 4096 tokens, HBM GB/s against 8 TB/s;
   - "kkt": the GDN chunk solve (reax_kkt) over 8192 tokens x 16 key heads, GB/s of k read + A written;
   - "howu": the GDN chunked forward (reax_howu) over 8 x 2048 tokens, 32 value heads, TFLOP/s of its chunk products;
+  - "gemm": the GEMM libraries at a Qwen3-MLP shape (4096 tokens, hidden 2560, intermediate 9728): reax_gv (gate/up
+    with the fused SiLU-times-up), reax_gemm (down projection) and reax_slices (the down projection as 4 fp32
+    split-K partials), each at its fastest config index, in TFLOP/s against the bf16 MFMA peak, beside torch.matmul
+    (hipBLASLt) on the same operands for reference;
   - "cpu_baseline": the OpenMP fp32 build of the CPU reference on a bounded sample of config 2's rows.
 Only N = 1 GPU is supported: the path is single-GPU by design.
 """
@@ -281,6 +285,54 @@ def bench_howu(torch, ops, iters=10):
     return ms, flops / (ms * 1e-3) / 1e12
 
 
+GEMM_M, GEMM_HID, GEMM_INTER, GEMM_S = 4096, 2560, 9728, 4
+
+
+def _time_ms(torch, run, iters, warm=30):
+    """Mean ms per call over `iters` back-to-back calls (one event pair), after `warm` untimed calls that bring the
+    clock up to its sustained rate."""
+    for _ in range(warm):
+        run()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        run()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def bench_gemm(torch, ops, iters=20):
+    """The three GEMM libraries at one MLP shape; each entry point is timed at the config indices that select
+    distinct tiles and reported at its fastest, with torch.matmul (hipBLASLt) of the same product beside it."""
+    M, Hd, I, S = GEMM_M, GEMM_HID, GEMM_INTER, GEMM_S
+    g_ = torch.Generator(device="cuda").manual_seed(7)
+    x = torch.randn((M, Hd), device="cuda", generator=g_).to(torch.bfloat16)
+    wg = (torch.randn((2 * I, Hd), device="cuda", generator=g_) * 0.05).to(torch.bfloat16)
+    h = torch.randn((M, I), device="cuda", generator=g_).to(torch.bfloat16)
+    wd = (torch.randn((Hd, I), device="cuda", generator=g_) * 0.05).to(torch.bfloat16)
+    act = torch.empty((M, I), dtype=torch.bfloat16, device="cuda")
+    d = torch.empty((M, Hd), dtype=torch.bfloat16, device="cuda")
+    p = torch.empty((S, M, Hd), dtype=torch.float32, device="cuda")
+    out = {}
+    # config indices covering the four tiles (128x128, 256x128, 128x256, 256x256) of each library
+    legs = [("gv", (2, 1, 0, 16), lambda c: ops.gv(x, wg, cfg=c, out=act), 2 * M * 2 * I * Hd,
+             lambda: torch.matmul(x, wg.t())),
+            ("plain", (2, 1, 0), lambda c: ops.gemm(h, wd, cfg=c, d=d), 2 * M * Hd * I, lambda: torch.matmul(h, wd.t())),
+            ("slices", (2, 1, 0), lambda c: ops.slices(h, wd, kps=I // S, S=S, cfg=c, p=p), 2 * M * Hd * I, None)]
+    for name, cfgs, run, flops, ref in legs:
+        best = min((_time_ms(torch, lambda: run(c), iters), c) for c in cfgs)
+        tf = flops / (best[0] * 1e-3) / 1e12
+        e = {"value": round(tf, 2), "unit": "TFLOP/s", "ms": round(best[0], 4), "cfg": best[1],
+             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": W.BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                          "frac": round(tf / W.BF16_PEAK_TFLOPS, 4)}}
+        if ref is not None:
+            e["hipblaslt_TFLOPs"] = round(flops / (_time_ms(torch, ref, iters) * 1e-3) / 1e12, 2)
+        out[name] = e
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -291,8 +343,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "rarn", "conv", "kkt", "howu"], help="run one leg only (for profiling)")
-    ap.add_argument("--no-gdn", action="store_true", help="skip the reax_rarn, reax_conv_l2 and reax_kkt legs")
+    ap.add_argument("--only", choices=["prefill", "decode", "rarn", "conv", "kkt", "howu", "gemm"],
+                    help="run one leg only (for profiling)")
+    ap.add_argument("--no-gdn", action="store_true", help="skip the rarn, conv, kkt, howu and gemm legs")
     ap.add_argument("--decode-splits", type=int, default=0, help="override config 4's key-split count")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 5 times: the reference kernel for scaling "
@@ -316,6 +369,9 @@ def main():
 
     from reax_fmha import ops
 
+    if args.only == "gemm":
+        print(json.dumps(bench_gemm(torch, ops)), flush=True)
+        return
     if args.only == "howu":
         ms, tf = bench_howu(torch, ops)
         print(json.dumps({"howu_TFLOPs": round(tf, 2), "ms": round(ms, 4), "seqs": HOWU_N, "tokens": HOWU_T}),
@@ -393,6 +449,9 @@ def main():
                         "value": round(tf, 2), "unit": "TFLOP/s", "ms": round(ms, 4),
                         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": W.BF16_PEAK_TFLOPS,
                                      "unit": "TFLOP/s", "frac": round(tf / W.BF16_PEAK_TFLOPS, 4)}}
+        g = bench_gemm(torch, ops)
+        line["gemm"] = {"workload": f"MLP {GEMM_M} tokens, hidden {GEMM_HID}, intermediate {GEMM_INTER}; slices S "
+                                    f"{GEMM_S} fp32", **g}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

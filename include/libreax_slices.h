@@ -10,12 +10,14 @@ extern "C" {
 
 /* Number of config indices reax_slices accepts (16, as gemm_slices_v2.cu:56). */
 int reax_slices_ncfg(void);
-/* Name of config c, "?" outside 0..15 (gemm_slices_v2.cu:57-64); here every index runs the same rocBLAS call. */
+/* Name of config c, "?" outside 0..15 (gemm_slices_v2.cu:57-64); here every index runs the one gfx950
+ * MFMA tile. */
 const char* reax_slices_cfgname(int c);
 /* Split-K partials: for s = 0..S-1, P[s][M][N] = X[:, s*kps .. (s+1)*kps) W[:, s*kps .. (s+1)*kps)^T with X [M][K]
  * and W [N][K] row-major, fp32 accumulation, each partial rounded once to fp32 (part_fp32 != 0) or bf16, partial s at
  * p + s*M*N elements. Replaces reax_slices, gemm_slices_v2.cu:65-84. Return codes as reax_gemm (9: unknown cfg; 1:
- * sizes <= 0, kps or K not a multiple of 8, N not a multiple of 8, S * kps > K, or a missing buffer). */
+ * sizes <= 0, kps or K not a multiple of 8, N not a multiple of 8, S * kps > K, S > 65535, a missing buffer or X / W
+ * not 16-byte aligned; 4: launch error). */
 int reax_slices(int cfg, int part_fp32, const void* x, const void* w, void* p, int M, int N, int kps, int S, int K,
                 void* stream);
 

@@ -9,7 +9,8 @@
 // that definition (an fp32 fast path with a double-precision fallback at bf16 rounding boundaries; the reference's
 // expf is accurate to about an ulp, so its bf16 SiLU can differ by one ulp in rare elements).
 //
-// Kernel: the shared matrix-core tile (gemm_tile.h, 128 x 128 tiles of C, K in slices of 64) with an epilogue that
+// Kernel: the shared matrix-core tiles (gemm_tile.h: 128 x 128 up to 256 x 256 tiles of C, K in slices of 64, the
+// config index picks the tile) with an epilogue that
 // pairs each gate column with the up column four to its right (four lanes over in the accumulator layout) and writes
 // only the activations: no intermediate buffer, like the reference's visitor.
 #include <hip/hip_runtime.h>
@@ -46,24 +47,26 @@ __device__ __forceinline__ float silu_bf16(float y) {
   return bfr(q);
 }
 
-__global__ void __launch_bounds__(gemm::THREADS) gv_kernel(const uint16_t* __restrict__ x,
-                                                           const uint16_t* __restrict__ w, uint16_t* __restrict__ out,
-                                                           int M, int N2, int K) {
-  __shared__ __align__(16) gemm::Lds S;
+template <class T>
+__global__ void __launch_bounds__(T::THREADS) gv_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                        uint16_t* __restrict__ out, int M, int N2, int K, int tiles_m,
+                                                        int tiles_n) {
+  __shared__ __align__(16) typename T::Lds S;
   const int NC = 2 * N2;  // columns of C
-  const int m_blk = blockIdx.y * gemm::BM, n_blk = blockIdx.x * gemm::BN;
-  f32x16_t acc[2][2];
-  gemm::mainloop(S, x, w, K, 0, K, M, NC, m_blk, n_blk, acc);
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int wm = 64 * (wv >> 1), wn = 64 * (wv & 1);
+  int tm, tn;
+  gemm::tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m_blk = tm * T::BM, n_blk = tn * T::BN;
+  typename T::Acc acc;
+  T::mainloop(S, x, w, K, 0, K, M, NC, m_blk, n_blk, acc);
+  const int lane = threadIdx.x & 63, wm = T::wm(), wn = T::wn();
 
   // ---- epilogue: element v of tile (a, b) is C[row][col] with row = wm + 32a + 8(v/4) + 4(lane/32) + v%4 and
   // col = wn + 32b + lane%32; gate columns have col % 8 < 4 and their up column is col + 4 (lane + 4)
   const int j = lane & 31;
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < T::WTM; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < T::WTN; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const float up = __shfl(acc[a][b][v], lane + 4 < 64 ? lane + 4 : lane, 64);
@@ -77,22 +80,29 @@ __global__ void __launch_bounds__(gemm::THREADS) gv_kernel(const uint16_t* __res
       }
 }
 
+template <class T>
+int launch_tile(const void* x, const void* w, void* out, int M, int N2, int K, void* stream) {
+  const int tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (2 * N2 + T::BN - 1) / T::BN;
+  hipLaunchKernelGGL(gv_kernel<T>, dim3((unsigned)(tiles_m * tiles_n)), dim3(T::THREADS), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
+                     static_cast<uint16_t*>(out), M, N2, K, tiles_m, tiles_n);
+  return hipGetLastError() == hipSuccess ? 0 : 3;  // gv:167
+}
+
 }  // namespace
 }  // namespace reax
 
 extern "C" {
 
+// tile of each config: the reference's threadblock shapes (gv:186-205) 128x256, 256x128, 128x128, 128x256, 128x256,
+// 256x128, 128x128, 128x128, 64x256, 128x256, 128x192, 128x192, 192x128, 192x128, 64x256, 64x256, 192x192, 128x128,
+// 128x128, 256x128, rounded to a gfx950 tile
+static const unsigned char kGvTile[20] = {2, 1, 0, 2, 2, 1, 0, 0, 2, 2, 2, 2, 1, 1, 2, 2, 3, 0, 0, 1};
+static const char* const kGvTileName[4] = {"mfma 128x128x64 4 waves", "mfma 256x128x64 8 waves",
+                                           "mfma 128x256x64 8 waves", "mfma 256x256x64 8 waves"};
+
 int reax_gv_ncfg(void) { return 20; }
-const char* reax_gv_cfgname(int c) {
-  static const char* n[] = {"mfma 128x128x64 cfg0",  "mfma 128x128x64 cfg1",  "mfma 128x128x64 cfg2",
-                            "mfma 128x128x64 cfg3",  "mfma 128x128x64 cfg4",  "mfma 128x128x64 cfg5",
-                            "mfma 128x128x64 cfg6",  "mfma 128x128x64 cfg7",  "mfma 128x128x64 cfg8",
-                            "mfma 128x128x64 cfg9",  "mfma 128x128x64 cfg10", "mfma 128x128x64 cfg11",
-                            "mfma 128x128x64 cfg12", "mfma 128x128x64 cfg13", "mfma 128x128x64 cfg14",
-                            "mfma 128x128x64 cfg15", "mfma 128x128x64 cfg16", "mfma 128x128x64 cfg17",
-                            "mfma 128x128x64 cfg18", "mfma 128x128x64 cfg19"};
-  return (c >= 0 && c < 20) ? n[c] : "?";
-}
+const char* reax_gv_cfgname(int c) { return (c >= 0 && c < 20) ? kGvTileName[kGvTile[c]] : "?"; }
 
 int reax_gv(int cfg, const void* x, const void* w, void* out, int M, int N2, int K, void* stream) {
   if (cfg < 0 || cfg >= 20) return 9;  // gv:207
@@ -102,11 +112,13 @@ int reax_gv(int cfg, const void* x, const void* w, void* out, int M, int N2, int
   if (M <= 0 || N2 <= 0 || K <= 0 || !x || !w || !out || (reinterpret_cast<uintptr_t>(x) & 15u) ||
       (reinterpret_cast<uintptr_t>(w) & 15u) || (reinterpret_cast<uintptr_t>(out) & 1u))
     return 3;
-  const dim3 grid((unsigned)((2LL * N2 + reax::gemm::BN - 1) / reax::gemm::BN), (unsigned)((M + reax::gemm::BM - 1) / reax::gemm::BM));
-  hipLaunchKernelGGL(reax::gv_kernel, grid, dim3(reax::gemm::THREADS), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), M,
-                     N2, K);
-  return hipGetLastError() == hipSuccess ? 0 : 3;  // gv:167
+  using namespace reax::gemm;
+  switch (kGvTile[cfg]) {
+    case kT256x128: return reax::launch_tile<T256x128>(x, w, out, M, N2, K, stream);
+    case kT128x256: return reax::launch_tile<T128x256>(x, w, out, M, N2, K, stream);
+    case kT256x256: return reax::launch_tile<T256x256>(x, w, out, M, N2, K, stream);
+    default: return reax::launch_tile<T128x128>(x, w, out, M, N2, K, stream);
+  }
 }
 
 }  // extern "C"

@@ -7,8 +7,10 @@
 //   slices: P[s][m][n] = X[m][s kps, (s+1) kps) . W[n][s kps, (s+1) kps)   P[s] row-major [M][N] at p + s M N,
 //           bf16 or fp32 (part_fp32)
 //
-// The reference selects one of 15 / 16 CUTLASS sm80 tile configurations by index, all with the same results; the
-// index is validated the same way here (an unknown index returns 9) and every index runs the one gfx950 tile.
+// The reference selects one of 15 / 16 CUTLASS sm80 tile configurations by index, all with the same results; here
+// index c runs the gfx950 tile (gemm_tile.h) nearest to the threadblock shape of the reference's config c, and all
+// tiles give the same bits too, so a caller that times every index and keeps the fastest still chooses among real
+// alternatives. An unknown index returns 9, as in the reference.
 // Shapes follow CUTLASS's can_implement for 8-wide bf16 accesses (code 1): positive sizes, K (kps) and the output
 // row stride multiples of 8; missing buffers and rows not 16-byte aligned also return 1 (the reference faults on
 // them). A failed launch returns 4, like the reference's trailing launch-error check.
@@ -33,25 +35,25 @@ namespace {
 __device__ __forceinline__ void put(float* o, float v) { *o = v; }
 __device__ __forceinline__ void put(uint16_t* o, float v) { *o = (uint16_t)(pack_bf16x2(v, 0.f) & 0xffffu); }
 
-// grid (ceil(N / 128), ceil(M / 128), S); slice s covers k in [s kext, (s + 1) kext) and writes out + s obs
-template <typename OutT>
-__global__ void __launch_bounds__(gemm::THREADS) gemm_kernel(const uint16_t* __restrict__ x,
-                                                             const uint16_t* __restrict__ w, OutT* __restrict__ out,
-                                                             int M, int N, int K, int kext, long long ldo,
-                                                             long long obs) {
-  __shared__ __align__(16) gemm::Lds S;
+// grid (tiles_m * tiles_n, 1, S); slice s covers k in [s kext, (s + 1) kext) and writes out + s obs
+template <class T, typename OutT>
+__global__ void __launch_bounds__(T::THREADS) gemm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+                                                          OutT* __restrict__ out, int M, int N, int K, int kext,
+                                                          long long ldo, long long obs, int tiles_m, int tiles_n) {
+  __shared__ __align__(16) typename T::Lds S;
   const int s = blockIdx.z;
-  const int m_blk = blockIdx.y * gemm::BM, n_blk = blockIdx.x * gemm::BN;
-  f32x16_t acc[2][2];
-  gemm::mainloop(S, x, w, K, s * kext, (s + 1) * kext, M, N, m_blk, n_blk, acc);
+  int tm, tn;
+  gemm::tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m_blk = tm * T::BM, n_blk = tn * T::BN;
+  typename T::Acc acc;
+  T::mainloop(S, x, w, K, s * kext, (s + 1) * kext, M, N, m_blk, n_blk, acc);
 
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int wm = 64 * (wv >> 1), wn = 64 * (wv & 1);
+  const int lane = threadIdx.x & 63, wm = T::wm(), wn = T::wn();
   OutT* o = out + s * obs;
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int a = 0; a < T::WTM; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+    for (int b = 0; b < T::WTN; ++b)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = m_blk + wm + 32 * a + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
@@ -62,15 +64,30 @@ __global__ void __launch_bounds__(gemm::THREADS) gemm_kernel(const uint16_t* __r
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <typename OutT>
-int launch(const void* x, const void* w, void* out, int M, int N, int K, int kext, int S, long long ldo,
-           long long obs, void* stream) {
-  const dim3 grid((unsigned)((N + gemm::BN - 1) / gemm::BN), (unsigned)((M + gemm::BM - 1) / gemm::BM), (unsigned)S);
-  hipLaunchKernelGGL(gemm_kernel<OutT>, grid, dim3(gemm::THREADS), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w), static_cast<OutT*>(out), M, N,
-                     K, kext, ldo, obs);
+template <class T, typename OutT>
+int launch_tile(const void* x, const void* w, void* out, int M, int N, int K, int kext, int S, long long ldo,
+                long long obs, void* stream) {
+  const int tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
+  hipLaunchKernelGGL((gemm_kernel<T, OutT>), dim3((unsigned)(tiles_m * tiles_n), 1, (unsigned)S), dim3(T::THREADS), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
+                     static_cast<OutT*>(out), M, N, K, kext, ldo, obs, tiles_m, tiles_n);
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
+
+template <typename OutT>
+int launch(int tile, const void* x, const void* w, void* out, int M, int N, int K, int kext, int S, long long ldo,
+           long long obs, void* stream) {
+  switch (tile) {
+    case gemm::kT256x128: return launch_tile<gemm::T256x128, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
+    case gemm::kT128x256: return launch_tile<gemm::T128x256, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
+    case gemm::kT256x256: return launch_tile<gemm::T256x256, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
+    default: return launch_tile<gemm::T128x128, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
+  }
+}
+
+// names of the tiles, by id
+const char* const kTileName[4] = {"mfma 128x128x64 4 waves", "mfma 256x128x64 8 waves", "mfma 128x256x64 8 waves",
+                                  "mfma 256x256x64 8 waves"};
 
 }  // namespace
 }  // namespace reax
@@ -78,35 +95,29 @@ int launch(const void* x, const void* w, void* out, int M, int N, int K, int kex
 extern "C" {
 
 #if defined(REAX_LIB_PLAIN)
+// tile of each config: the reference's threadblock shapes (gemm_plain2.cu:40-54) 128x256, 256x128, 128x128, 128x256,
+// 128x256, 192x128, 192x128, 64x256, 64x256, 128x128, 128x128, 256x128, 256x64, 128x64, 64x128, rounded to a gfx950 tile
+static const unsigned char kPlainTile[15] = {2, 1, 0, 2, 2, 1, 1, 2, 2, 0, 0, 1, 1, 0, 0};
+
 int reax_gemm_ncfg(void) { return 15; }
-const char* reax_gemm_cfgname(int c) {
-  static const char* n[] = {"mfma 128x128x64 cfg0",  "mfma 128x128x64 cfg1",  "mfma 128x128x64 cfg2",
-                            "mfma 128x128x64 cfg3",  "mfma 128x128x64 cfg4",  "mfma 128x128x64 cfg5",
-                            "mfma 128x128x64 cfg6",  "mfma 128x128x64 cfg7",  "mfma 128x128x64 cfg8",
-                            "mfma 128x128x64 cfg9",  "mfma 128x128x64 cfg10", "mfma 128x128x64 cfg11",
-                            "mfma 128x128x64 cfg12", "mfma 128x128x64 cfg13", "mfma 128x128x64 cfg14"};
-  return (c >= 0 && c < 15) ? n[c] : "?";
-}
+const char* reax_gemm_cfgname(int c) { return (c >= 0 && c < 15) ? reax::kTileName[kPlainTile[c]] : "?"; }
 
 int reax_gemm(int cfg, const void* x, const void* w, void* d, int M, int N, int K, int ldd, void* stream) {
   if (cfg < 0 || cfg >= 15) return 9;  // gemm_plain2.cu:56
   if (M <= 0 || N <= 0 || K <= 0 || K % 8 || ldd % 8 || ldd < N || !x || !w || !d || !reax::aligned16(x) ||
       !reax::aligned16(w) || (reinterpret_cast<uintptr_t>(d) & 1u))
     return 1;  // can_implement (gemm_plain2.cu:24)
-  return reax::launch<uint16_t>(x, w, d, M, N, K, K, 1, ldd, 0, stream);
+  return reax::launch<uint16_t>(kPlainTile[cfg], x, w, d, M, N, K, K, 1, ldd, 0, stream);
 }
 
 #else
+// tile of each config: the reference's threadblock shapes (gemm_slices_v2.cu:38-53) 128x256, 256x128, 128x128,
+// 64x256, 128x128, 256x128, 128x256, 64x128, 128x64, 64x256, 64x128, 256x64, 128x128, 128x128, 64x128, 256x128,
+// rounded to a gfx950 tile
+static const unsigned char kSlicesTile[16] = {2, 1, 0, 2, 0, 1, 2, 0, 0, 2, 0, 1, 0, 0, 0, 1};
+
 int reax_slices_ncfg(void) { return 16; }
-const char* reax_slices_cfgname(int c) {
-  static const char* n[] = {"mfma 128x128x64 cfg0",  "mfma 128x128x64 cfg1",  "mfma 128x128x64 cfg2",
-                            "mfma 128x128x64 cfg3",  "mfma 128x128x64 cfg4",  "mfma 128x128x64 cfg5",
-                            "mfma 128x128x64 cfg6",  "mfma 128x128x64 cfg7",  "mfma 128x128x64 cfg8",
-                            "mfma 128x128x64 cfg9",  "mfma 128x128x64 cfg10", "mfma 128x128x64 cfg11",
-                            "mfma 128x128x64 cfg12", "mfma 128x128x64 cfg13", "mfma 128x128x64 cfg14",
-                            "mfma 128x128x64 cfg15"};
-  return (c >= 0 && c < 16) ? n[c] : "?";
-}
+const char* reax_slices_cfgname(int c) { return (c >= 0 && c < 16) ? reax::kTileName[kSlicesTile[c]] : "?"; }
 
 int reax_slices(int cfg, int part_fp32, const void* x, const void* w, void* p, int M, int N, int kps, int S, int K,
                 void* stream) {
@@ -116,8 +127,8 @@ int reax_slices(int cfg, int part_fp32, const void* x, const void* w, void* p, i
       (reinterpret_cast<uintptr_t>(p) & (part_fp32 ? 3u : 1u)))
     return 1;  // can_implement (gemm_slices_v2.cu:29)
   const long long obs = (long long)M * N;
-  return part_fp32 ? reax::launch<float>(x, w, p, M, N, K, kps, S, N, obs, stream)
-                   : reax::launch<uint16_t>(x, w, p, M, N, K, kps, S, N, obs, stream);
+  return part_fp32 ? reax::launch<float>(kSlicesTile[cfg], x, w, p, M, N, K, kps, S, N, obs, stream)
+                   : reax::launch<uint16_t>(kSlicesTile[cfg], x, w, p, M, N, K, kps, S, N, obs, stream);
 }
 #endif
 

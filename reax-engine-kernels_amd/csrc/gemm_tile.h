@@ -1,18 +1,19 @@
-// The matrix-core tile shared by the GEMM libraries (libreax_plain.so, libreax_slices.so, libreax_gv.so):
-//   C[m][n] = sum_{k0 <= k < k1} X[m][k] W[n][k]   for one 128 x 128 tile of C
+// The matrix-core tiles shared by the GEMM libraries (libreax_plain.so, libreax_slices.so, libreax_gv.so):
+//   C[m][n] = sum_{k0 <= k < k1} X[m][k] W[n][k]   for one BM x BN tile of C
 // with X [.][ldx] and W [.][ldx] row-major bf16 (both operands K-contiguous), fp32 accumulation.
 //
-// 256 threads (4 wavefronts), each wavefront a 64 x 64 quarter of the tile as 2 x 2 v_mfma_f32_32x32x16_bf16
-// tiles. K advances 64 at a time: the 128 x 64 slices of X and W live in LDS (16-byte units XOR-swizzled by row,
-// so every MFMA fragment is one conflict-free 16-byte read), double-buffered, and the next slice is read from
-// global memory into registers while the current one is multiplied (one barrier per slice). Rows beyond M or N and
-// k units at or beyond k1 read as zeros; k0 and k1 are multiples of 8 (whole 16-byte units).
+// A tile is NWM x NWN wavefronts, each a (32 WTM) x (32 WTN) block of C as WTM x WTN v_mfma_f32_32x32x16_bf16
+// tiles, so that one 16-deep step reads WTM + WTN fragments for WTM * WTN MFMAs (larger wave blocks need less LDS
+// bandwidth per MFMA). K advances 64 at a time: the BM x 64 and BN x 64 slices of X and W live in LDS (16-byte units
+// XOR-swizzled by row, so every MFMA fragment is one conflict-free 16-byte read), double-buffered, and the next
+// slice is read from global memory into registers while the current one is multiplied (one barrier per slice). Rows
+// beyond M or N and k units at or beyond k1 read as zeros; k0 and k1 are multiples of 8 (whole 16-byte units).
 //
-// Each accumulator adds its K slices in ascending order (the MFMA sums 16 products per step), so results agree with
-// any fp32-accumulated product to fp32 accumulation accuracy; they are not bit-identical to another order.
+// Every tile shape adds each accumulator's K slices in the same ascending order of 16-element MFMA steps, so all
+// shapes give identical bits; against another summation order results agree to fp32 accumulation accuracy.
 //
 // Accumulator layout: element v of acc[a][b] is C[wm + 32a + 8(v/4) + 4(lane/32) + v%4][wn + 32b + lane%32]
-// relative to the tile, with wm = 64 (wave / 2), wn = 64 (wave % 2).
+// relative to the tile, with wm = 32 WTM (wave / NWN), wn = 32 WTN (wave % NWN).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -23,77 +24,126 @@
 namespace reax {
 namespace gemm {
 
-constexpr int BM = 128, BN = 128, BK = 64, THREADS = 256;
-constexpr int UNITS = BK / 8;                       // 16-byte units per slice row
-constexpr int LOADS = BM * UNITS / THREADS;         // units per thread per operand per slice (4)
-static_assert(BM == BN && BM * UNITS % THREADS == 0, "one staging pattern serves both operands");
+constexpr int BK = 64;
+constexpr int UNITS = BK / 8;  // 16-byte units per slice row
 
-struct Lds {
-  uint16_t xs[2][BM * BK];
-  uint16_t ws[2][BN * BK];
-};
-
-// element offset of (row r, unit u) in a 128 x 64 slice
+// element offset of (row r, unit u) in a slice of rows of 64: units XOR row % 8, so 8 consecutive rows read by one
+// fragment use 8 distinct 16-byte columns
 __device__ __forceinline__ int slot(int r, int u) { return r * BK + ((u ^ (r & (UNITS - 1))) << 3); }
 
-__device__ __forceinline__ void mainloop(Lds& S, const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-                                         long long ldx, int k0, int k1, int M, int N, int m_blk, int n_blk,
-                                         f32x16_t (&acc)[2][2]) {
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int wm = 64 * (wv >> 1), wn = 64 * (wv & 1);
-  u32x4_t rx[LOADS], rw[LOADS];
-  auto load = [&](int kb) __attribute__((always_inline)) {
-#pragma unroll
-    for (int e = 0; e < LOADS; ++e) {
-      const int i = tid + THREADS * e, r = i / UNITS, u = i % UNITS, k = kb + 8 * u;
-      const int gm = m_blk + r, gn = n_blk + r;
-      rx[e] = (gm < M && k < k1) ? *reinterpret_cast<const u32x4_t*>(x + gm * ldx + k) : u32x4_t{0u, 0u, 0u, 0u};
-      rw[e] = (gn < N && k < k1) ? *reinterpret_cast<const u32x4_t*>(w + gn * ldx + k) : u32x4_t{0u, 0u, 0u, 0u};
-    }
+template <int NWM_, int NWN_, int WTM_, int WTN_>
+struct Tile {
+  static constexpr int NWM = NWM_, NWN = NWN_, WTM = WTM_, WTN = WTN_;
+  static constexpr int THREADS = 64 * NWM * NWN;
+  static constexpr int BM = 32 * WTM * NWM, BN = 32 * WTN * NWN;
+  static constexpr int LX = BM * UNITS / THREADS, LW = BN * UNITS / THREADS;  // staged units per thread
+  static_assert(BM * UNITS % THREADS == 0 && BN * UNITS % THREADS == 0, "whole units per thread");
+
+  struct Lds {
+    uint16_t xs[2][BM * BK];
+    uint16_t ws[2][BN * BK];
   };
-  auto store = [&](int buf) __attribute__((always_inline)) {
+  using Acc = f32x16_t[WTM][WTN];
+
+  __device__ static int wm() { return 32 * WTM * ((int)(threadIdx.x >> 6) / NWN); }
+  __device__ static int wn() { return 32 * WTN * ((int)(threadIdx.x >> 6) % NWN); }
+
+  __device__ __forceinline__ static void mainloop(Lds& S, const uint16_t* __restrict__ x,
+                                                  const uint16_t* __restrict__ w, long long ldx, int k0, int k1,
+                                                  int M, int N, int m_blk, int n_blk, Acc& acc) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wm0 = wm(), wn0 = wn();
+    struct Regs {
+      u32x4_t x[LX], w[LW];
+    };
+    auto load = [&](Regs& R, int kb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int e = 0; e < LOADS; ++e) {
-      const int i = tid + THREADS * e, r = i / UNITS, u = i % UNITS;
-      *reinterpret_cast<u32x4_t*>(&S.xs[buf][slot(r, u)]) = rx[e];
-      *reinterpret_cast<u32x4_t*>(&S.ws[buf][slot(r, u)]) = rw[e];
-    }
-  };
+      for (int e = 0; e < LX; ++e) {
+        const int i = tid + THREADS * e, r = i / UNITS, k = kb + 8 * (i % UNITS), gm = m_blk + r;
+        R.x[e] = (gm < M && k < k1) ? *reinterpret_cast<const u32x4_t*>(x + gm * ldx + k) : u32x4_t{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int e = 0; e < LW; ++e) {
+        const int i = tid + THREADS * e, r = i / UNITS, k = kb + 8 * (i % UNITS), gn = n_blk + r;
+        R.w[e] = (gn < N && k < k1) ? *reinterpret_cast<const u32x4_t*>(w + gn * ldx + k) : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    };
+    auto store = [&](const Regs& R, int buf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int e = 0; e < LX; ++e) {
+        const int i = tid + THREADS * e;
+        *reinterpret_cast<u32x4_t*>(&S.xs[buf][slot(i / UNITS, i % UNITS)]) = R.x[e];
+      }
+#pragma unroll
+      for (int e = 0; e < LW; ++e) {
+        const int i = tid + THREADS * e;
+        *reinterpret_cast<u32x4_t*>(&S.ws[buf][slot(i / UNITS, i % UNITS)]) = R.w[e];
+      }
+    };
+    auto compute = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        const int u = 2 * ks + (lane >> 5), r = lane & 31;
+        bf16x8_t af[WTM], bf[WTN];
+#pragma unroll
+        for (int a = 0; a < WTM; ++a)
+          af[a] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&S.xs[buf][slot(wm0 + 32 * a + r, u)]));
+#pragma unroll
+        for (int b = 0; b < WTN; ++b)
+          bf[b] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&S.ws[buf][slot(wn0 + 32 * b + r, u)]));
+#pragma unroll
+        for (int a = 0; a < WTM; ++a)
+#pragma unroll
+          for (int b = 0; b < WTN; ++b) acc[a][b] = mfma32(af[a], bf[b], acc[a][b]);
+      }
+    };
 
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < WTM; ++a)
 #pragma unroll
-    for (int b = 0; b < 2; ++b)
+      for (int b = 0; b < WTN; ++b)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+        for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
 
-  const int nk = (k1 - k0 + BK - 1) / BK;
-  load(k0);
-  store(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) load(k0 + (kt + 1) * BK);
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int u = 2 * ks + (lane >> 5), r = lane & 31;
-      bf16x8_t af[2], bf[2];
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-        af[a] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&S.xs[buf][slot(wm + 32 * a + r, u)]));
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-        bf[b] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&S.ws[buf][slot(wn + 32 * b + r, u)]));
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int b = 0; b < 2; ++b) acc[a][b] = mfma32(af[a], bf[b], acc[a][b]);
-    }
-    if (kt + 1 < nk) {
-      store(buf ^ 1);  // the other buffer was last read in the previous iteration, before its closing barrier
-      __syncthreads();
+    // slice kt + 1 is read into registers while slice kt (LDS buffer kt % 2) is multiplied. Reading two slices
+    // ahead (a second register set) measured slower on every shape: the loads arrive in time already.
+    const int nk = (k1 - k0 + BK - 1) / BK;
+    Regs R;
+    load(R, k0);
+    store(R, 0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + 1 < nk) load(R, k0 + (kt + 1) * BK);
+      compute(kt & 1);
+      if (kt + 1 < nk) {
+        store(R, (kt + 1) & 1);  // buffer (kt + 1) % 2 was last read in step kt - 1, before its closing barrier
+        __syncthreads();
+      }
     }
   }
+};
+
+// The tile shapes a config index can select. 128 x 128 runs 4 wavefronts of 64 x 64 (two workgroups per CU, 64 KB
+// LDS each); the larger tiles run 8 wavefronts (one workgroup per CU, 96 or 128 KB LDS), which halves (256 x 256)
+// or cuts by a quarter the operand bytes per MFMA read through L2.
+using T128x128 = Tile<2, 2, 2, 2>;
+using T256x128 = Tile<4, 2, 2, 2>;
+using T128x256 = Tile<2, 4, 2, 2>;
+using T256x256 = Tile<2, 4, 4, 2>;
+enum TileId : unsigned char { kT128x128 = 0, kT256x128 = 1, kT128x256 = 2, kT256x256 = 3 };
+
+// XCD-aware tile order: hardware hands consecutive workgroups to the 8 XCDs in turn, so workgroup b runs on XCD
+// b % 8. When the tile count is a multiple of 8, each XCD is given a contiguous range of the tile sequence; the
+// sequence walks columns of GROUP_M tile rows, so the workgroups resident on one XCD share X rows and W rows in that
+// XCD's L2. A bijection of [0, tiles_m * tiles_n) onto the tile grid.
+__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int& tm, int& tn) {
+  constexpr int XCDS = 8, GROUP_M = 8;
+  const int nb = tiles_m * tiles_n;
+  const int t = nb % XCDS == 0 ? (b % XCDS) * (nb / XCDS) + b / XCDS : b;
+  const int per_group = GROUP_M * tiles_n;
+  const int first_m = (t / per_group) * GROUP_M, rows = min(tiles_m - first_m, GROUP_M), i = t % per_group;
+  tm = first_m + i % rows;
+  tn = i / rows;
 }
 
 }  // namespace gemm

@@ -227,3 +227,60 @@ def howu_norm(q, k, v, beta, A, g, cu, f2s, z, nw, *, N, H, HV, scale, eps, fact
                                    f2s.data_ptr(), z.data_ptr(), z.stride(0), nw.data_ptr(), eps, factor)
     _check("reax_howu_norm", rc)
     return out
+
+
+# ---------------------------------------------------------------------------------------------- GEMM libraries
+
+def _rowmajor_bf16(*ts):
+    for t in ts:
+        if t.dtype != torch.bfloat16 or t.dim() != 2 or t.stride(1) != 1 or t.stride(0) != t.shape[1]:
+            raise ValueError("GEMM operands are contiguous row-major bf16 matrices")
+
+
+def gemm(x, w, *, cfg=0, d=None):
+    """reax_gemm (libreax_plain/gemm_plain2.cu:37-56): d = bf16(x w^T), x bf16 [M][K], w bf16 [N][K]; d bf16 [M][ldd]
+    with ldd >= N (allocated [M][N] if None; its row stride is d.stride(0)). Returns d."""
+    _dev(x, w, d)
+    _rowmajor_bf16(x, w)
+    M, K = x.shape
+    N = w.shape[0]
+    if d is None:
+        d = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    if d.dtype != torch.bfloat16 or d.stride(1) != 1 or d.shape[0] != M or d.shape[1] < N:
+        raise ValueError("d must be bf16 [M][>= N] with unit column stride")
+    _check("reax_gemm", abi.plain().reax_gemm(cfg, x.data_ptr(), w.data_ptr(), d.data_ptr(), M, N, K, d.stride(0),
+                                              _stream()))
+    return d
+
+
+def slices(x, w, *, kps, S, part_fp32=True, cfg=0, p=None):
+    """reax_slices (libreax_slices/gemm_slices_v2.cu:65-84): the split-K partials p[s] = x[:, s kps:(s+1) kps]
+    w[:, s kps:(s+1) kps]^T for s < S, fp32 or bf16 [S][M][N] (allocated if None). Returns p."""
+    _dev(x, w, p)
+    _rowmajor_bf16(x, w)
+    M, K = x.shape
+    N = w.shape[0]
+    dt = torch.float32 if part_fp32 else torch.bfloat16
+    if p is None:
+        p = torch.empty((S, M, N), dtype=dt, device=x.device)
+    if p.dtype != dt or not p.is_contiguous() or tuple(p.shape) != (S, M, N):
+        raise ValueError(f"p must be contiguous {dt} [S][M][N]")
+    _check("reax_slices", abi.slices().reax_slices(cfg, int(part_fp32), x.data_ptr(), w.data_ptr(), p.data_ptr(), M,
+                                                   N, kps, S, K, _stream()))
+    return p
+
+
+def gv(x, w_g4, *, cfg=0, out=None):
+    """reax_gv (libreax_gv/gateup_vis2.cu:184-208): out = bf16(bf16(silu(bf16 g)) bf16 u) with g, u the gate and up
+    columns of x w_g4^T, w_g4 bf16 [2 N2][K] holding gate and up rows interleaved in groups of 4. Returns out,
+    bf16 [M][N2]."""
+    _dev(x, w_g4, out)
+    _rowmajor_bf16(x, w_g4)
+    M, K = x.shape
+    N2 = w_g4.shape[0] // 2
+    if out is None:
+        out = torch.empty((M, N2), dtype=torch.bfloat16, device=x.device)
+    if out.dtype != torch.bfloat16 or not out.is_contiguous() or tuple(out.shape) != (M, N2):
+        raise ValueError("out must be contiguous bf16 [M][N2]")
+    _check("reax_gv", abi.gv().reax_gv(cfg, x.data_ptr(), w_g4.data_ptr(), out.data_ptr(), M, N2, K, _stream()))
+    return out

@@ -55,6 +55,36 @@ def test_plain_gemm(M, N, K, ldd, cfg):
     assert bad == 0, f"{bad} outputs off (max error {rel:.3g} of the scale)"
 
 
+@pytest.mark.parametrize("lib", ["plain", "slices", "gv"])
+def test_configs_bit_identical(lib):
+    """Every config index (tile shape) adds each output's K terms in the same order: identical bits (the reference's
+    configs share one reduction order too, gemm_slices_v2.cu:5-8)."""
+    from reax_fmha import abi
+
+    M, N, K = 300, 264, 392
+    x, w = _rand((M, K), 7), _rand((N, K), 8, 0.1)
+    dx, dw = W.bits_to_torch(x, "cuda"), W.bits_to_torch(w, "cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    outs = []
+    ncfg = {"plain": 15, "slices": 16, "gv": 20}[lib]
+    for cfg in range(ncfg):
+        _say(f"{lib} cfg={cfg}")
+        if lib == "plain":
+            o = torch.zeros((M, N), dtype=torch.bfloat16, device="cuda")
+            rc = abi.plain().reax_gemm(cfg, dx.data_ptr(), dw.data_ptr(), o.data_ptr(), M, N, K, N, st)
+        elif lib == "slices":
+            o = torch.zeros((2, M, N), dtype=torch.float32, device="cuda")
+            rc = abi.slices().reax_slices(cfg, 1, dx.data_ptr(), dw.data_ptr(), o.data_ptr(), M, N, 192, 2, K, st)
+        else:
+            o = torch.zeros((M, N // 2), dtype=torch.bfloat16, device="cuda")
+            rc = abi.gv().reax_gv(cfg, dx.data_ptr(), dw.data_ptr(), o.data_ptr(), M, N // 2, K, st)
+        torch.cuda.synchronize()
+        assert rc == 0
+        outs.append(o.view(torch.int16 if o.dtype == torch.bfloat16 else torch.int32).cpu().numpy())
+    for cfg in range(1, ncfg):
+        assert np.array_equal(outs[cfg], outs[0]), f"config {cfg} differs from config 0"
+
+
 @pytest.mark.parametrize("part_fp32", [1, 0])
 @pytest.mark.parametrize("M,N,kps,S,K", [(64, 128, 256, 4, 1024), (200, 72, 64, 3, 200), (64, 128, 64, 2, 128),
                                           (130, 256, 520, 1, 520)])
@@ -67,7 +97,7 @@ def test_slices(M, N, kps, S, K, part_fp32):
     dt = torch.float32 if part_fp32 else torch.bfloat16
     p = torch.zeros((S, M, N), dtype=dt, device="cuda")
     dx, dw = W.bits_to_torch(x, "cuda"), W.bits_to_torch(w, "cuda")  # held: a freed temporary's block is reused
-    rc = abi.slices().reax_slices(0, part_fp32, dx.data_ptr(), dw.data_ptr(), p.data_ptr(), M, N, kps, S, K,
+    rc = abi.slices().reax_slices(kps // 8 % 4, part_fp32, dx.data_ptr(), dw.data_ptr(), p.data_ptr(), M, N, kps, S, K,
                                   torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert rc == 0
@@ -78,11 +108,12 @@ def test_slices(M, N, kps, S, K, part_fp32):
         assert bad == 0, f"slice {s}: {bad} partials off (max error {rel:.3g} of the scale)"
 
 
-@pytest.mark.parametrize("M,N2,K", [(128, 64, 256), (77, 100, 520), (512, 1024, 2560)])
-def test_gv(M, N2, K):
+@pytest.mark.parametrize("M,N2,K,cfg", [(128, 64, 256, 0), (77, 100, 520, 1), (512, 1024, 2560, 2), (300, 260, 64, 3),
+                                        (130, 516, 136, 0)])
+def test_gv(M, N2, K, cfg):
     from reax_fmha import abi
 
-    _say(f"gv M={M} N2={N2} K={K}")
+    _say(f"gv M={M} N2={N2} K={K} cfg={cfg}")
     x, w = _rand((M, K), 5, 0.5), _rand((2 * N2, K), 6, 0.05)
     c = bf16_to_f32(x).astype(np.float64) @ bf16_to_f32(w).astype(np.float64).T      # [M][2 N2]
     cg = c.reshape(M, N2 // 4, 2, 4)
@@ -92,7 +123,7 @@ def test_gv(M, N2, K):
     ref = (s * u).reshape(M, N2)
     out = torch.full((M, N2), float("nan"), dtype=torch.bfloat16, device="cuda")
     dx, dw = W.bits_to_torch(x, "cuda"), W.bits_to_torch(w, "cuda")
-    rc = abi.gv().reax_gv(0, dx.data_ptr(), dw.data_ptr(), out.data_ptr(), M, N2, K,
+    rc = abi.gv().reax_gv(cfg, dx.data_ptr(), dw.data_ptr(), out.data_ptr(), M, N2, K,
                           torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert rc == 0
