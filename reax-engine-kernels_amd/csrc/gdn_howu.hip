@@ -38,10 +38,14 @@ namespace {
 
 constexpr int HW_BT = 64, HW_D = 128, HW_THREADS = 256;
 
-// element (r, c) of a row-major bf16 matrix W columns wide, 16-byte units XOR-swizzled by the row
+// element (r, c) of a row-major bf16 matrix W columns wide, 16-byte units XOR-swizzled by the row. Rows of 64
+// (128 bytes, two per 256-byte line of the 64 banks) also mix row / 8 into the XOR: fragment reads of 16
+// consecutive rows then use 16 distinct bank groups, and the transposed 2-byte stores of 16 rows 8 apart (the
+// staging of k^T, vb^T, kb^T) spread over 8 of them instead of one.
 template <int W>
 __device__ __forceinline__ int sw(int r, int c) {
-  return r * W + ((((c >> 3) ^ (r & (W / 8 - 1)))) << 3) + (c & 7);
+  const int f = W == 64 ? (r ^ (r >> 3)) & 7 : r & (W / 8 - 1);
+  return r * W + (((c >> 3) ^ f) << 3) + (c & 7);
 }
 
 struct HowuLds {
