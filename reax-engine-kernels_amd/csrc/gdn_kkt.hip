@@ -6,14 +6,17 @@
 //
 // The reference forms k k^T with bf16 tensor-core MMAs, the decay with the approximate ex2, the 16 x 16 diagonal
 // inverses by forward substitution and the off-diagonal blocks with tf32 MMAs (10-bit mantissa operands). This build
-// computes the same quantities in fp32 throughout (exact bf16 products, v_exp_f32, full-precision forward
-// substitution), so its results are at least as close to the exact inverse; agreement with the reference is to
-// its own tf32/bf16 accuracy, not bit for bit.
+// forms k k^T on the matrix cores too (bf16 products are exact, fp32 accumulation) and the rest in fp32
+// (v_exp_f32, full-precision forward substitution), so its results are at least as close to the exact inverse;
+// agreement with the reference is to its own tf32/bf16 accuracy, not bit for bit.
 //
-// Layout: one workgroup of 256 threads per (chunk, key head). Phase 1 stages the chunk's k (64 x 128) in LDS as
-// fp32; phase 2 forms the lower half of k k^T (each thread a 4 x 4 block, 128-long dot products); phase 3 applies
-// decay, mask and beta for both value heads; phase 4 solves (I + M) X = I column by column (128 threads: 2 heads x
-// 64 columns, the column in registers, M read by broadcast); phase 5 writes the bf16 rows.
+// Layout: one workgroup of 256 threads per (chunk, key head), 52 KB of LDS so that three workgroups share a CU and
+// one's solve overlaps the others' loads and products. Phase 1 stages the chunk's k (64 x 128 bf16, 16-byte units XOR-swizzled by row),
+// g and beta; phase 2 forms k k^T with v_mfma_f32_32x32x16_bf16 (wavefronts 0-2: the two diagonal 32 x 32 tiles and
+// the one below them) and writes M for both value heads straight from the accumulators (decay, mask and beta);
+// phase 3 solves (I + M) X = I column by column (128 threads: 2 heads x 64 columns, the column in registers, M read
+// by broadcast) and writes each column's bf16 entries straight to A (a wavefront's 64 lanes hold 64 adjacent
+// columns of one row: 128 contiguous bytes per store).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -27,24 +30,26 @@ namespace reax {
 namespace {
 
 constexpr int KKT_BT = 64, KKT_K = 128, KKT_THREADS = 256;
-constexpr int KKT_LD = KKT_BT + 1;  // padded row of the 64 x 64 fp32 matrices
+
+__device__ __forceinline__ uint16_t bf16_bits(float x) { return (uint16_t)(pack_bf16x2(x, 0.f) & 0xffffu); }
 constexpr int KKT_LDM = KKT_BT + 4;  // rows of M: 16-byte aligned, read 4 entries at a time by broadcast
 
 struct KktLds {
-  float k[KKT_BT][KKT_K + 4];  // padded rows: the 4 x 4 block reads of phase 2 spread over the banks
-  float raw[KKT_BT][KKT_LD];
+  uint16_t k[KKT_BT * KKT_K];  // k rows, 16-byte units XOR-swizzled by row
   float m[2][KKT_BT][KKT_LDM];
-  float x[2][KKT_BT][KKT_LD];
   float g[2][KKT_BT];
   float beta[2][KKT_BT];
 };
 
-__global__ void __launch_bounds__(KKT_THREADS) kkt_kernel(const uint16_t* __restrict__ k, const float* __restrict__ g,
-                                                          const uint16_t* __restrict__ beta, uint16_t* __restrict__ A,
-                                                          const int64_t* __restrict__ cu,
-                                                          const int64_t* __restrict__ cidx, int H, int HV) {
+// element (r, c) of the staged k: 16 units of 8 per row, unit index XOR row % 16
+__device__ __forceinline__ int ksw(int r, int c) { return r * KKT_K + ((((c >> 3) ^ (r & 15))) << 3) + (c & 7); }
+
+__global__ void __launch_bounds__(KKT_THREADS, 3) kkt_kernel(const uint16_t* __restrict__ k, const float* __restrict__ g,
+                                                             const uint16_t* __restrict__ beta, uint16_t* __restrict__ A,
+                                                             const int64_t* __restrict__ cu,
+                                                             const int64_t* __restrict__ cidx, int H, int HV) {
   __shared__ __align__(16) KktLds S;
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int i_n = (int)cidx[2 * (long long)blockIdx.x], i_t = (int)cidx[2 * (long long)blockIdx.x + 1];
   const int kh = blockIdx.y;
   const long long bos = cu[i_n];
@@ -53,15 +58,12 @@ __global__ void __launch_bounds__(KKT_THREADS) kkt_kernel(const uint16_t* __rest
   const int nval = min(KKT_BT, T - t0);
 
   // ---- phase 1: k rows (zero beyond the chunk's valid rows), g and beta of the two value heads
-  for (int i = tid; i < KKT_BT * (KKT_K / 8); i += KKT_THREADS) {
-    const int r = i >> 4, c8 = (i & 15) * 8;
+#pragma unroll
+  for (int e = 0; e < KKT_BT * (KKT_K / 8) / KKT_THREADS; ++e) {
+    const int i = tid + KKT_THREADS * e, r = i >> 4, c8 = (i & 15) * 8;
     u32x4_t w = {0u, 0u, 0u, 0u};
     if (r < nval) w = *reinterpret_cast<const u32x4_t*>(k + ((bos + t0 + r) * H + kh) * KKT_K + c8);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      S.k[r][c8 + 2 * q] = bf16lo(w[q]);
-      S.k[r][c8 + 2 * q + 1] = bf16hi(w[q]);
-    }
+    *reinterpret_cast<u32x4_t*>(S.k + ksw(r, c8)) = w;
   }
   if (tid < 2 * KKT_BT) {
     const int v = tid >> 6, r = tid & 63, hv = 2 * kh + v;
@@ -70,50 +72,40 @@ __global__ void __launch_bounds__(KKT_THREADS) kkt_kernel(const uint16_t* __rest
   }
   __syncthreads();
 
-  // ---- phase 2: raw = k k^T on and below the diagonal, a 4 x 4 block per thread
-  {
-    const int bi = tid >> 4, bj = tid & 15;
-    if (bj <= bi) {
-      float acc[4][4];
+  // ---- phase 2: k k^T on the matrix cores for the tiles on and below the diagonal (wavefront 0: rows and columns
+  // 0-31, 1: rows 32-63 x columns 0-31, 2: rows and columns 32-63), then M[v][r][c] = (k_r . k_c) 2^(g_r - g_c)
+  // beta_r for c < r < nval, else 0 (entries on or above the diagonal are never read by the solve)
+  if (wv < 3) {
+    const int I = wv == 0 ? 0 : 1, J = wv == 2 ? 1 : 0;
+    const int rr = lane & 31, kq = 8 * (lane >> 5);
+    f32x16_t acc = {};
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+    for (int s = 0; s < KKT_K / 16; ++s) {
+      const bf16x8_t a = as_bf16x8(*reinterpret_cast<const u32x4_t*>(S.k + ksw(32 * I + rr, 16 * s + kq)));
+      const bf16x8_t b = as_bf16x8(*reinterpret_cast<const u32x4_t*>(S.k + ksw(32 * J + rr, 16 * s + kq)));
+      acc = mfma32(a, b, acc);
+    }
+    const int c = 32 * J + rr;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = 0.f;
-      for (int c = 0; c < KKT_K; c += 4) {
-        f32x4_t ra[4], rb[4];
+    for (int e = 0; e < 16; ++e) {
+      const int r = 32 * I + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+      const bool live = c < r && r < nval;
 #pragma unroll
-        for (int a = 0; a < 4; ++a) ra[a] = *reinterpret_cast<const f32x4_t*>(&S.k[4 * bi + a][c]);
-#pragma unroll
-        for (int b = 0; b < 4; ++b) rb[b] = *reinterpret_cast<const f32x4_t*>(&S.k[4 * bj + b][c]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-          for (int a = 0; a < 4; ++a)
-#pragma unroll
-            for (int b = 0; b < 4; ++b) acc[a][b] = __builtin_fmaf(ra[a][e], rb[b][e], acc[a][b]);
-      }
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) S.raw[4 * bi + a][4 * bj + b] = acc[a][b];
+      for (int v = 0; v < 2; ++v)
+        S.m[v][r][c] = live ? (acc[e] * fast_exp2(S.g[v][r] - S.g[v][c])) * S.beta[v][r] : 0.f;
     }
   }
   __syncthreads();
 
-  // ---- phase 3: M for both value heads (strictly lower, valid rows only): raw * 2^(g_r - g_c) * beta_r
-  for (int i = tid; i < 2 * KKT_BT * KKT_BT; i += KKT_THREADS) {
-    const int v = i >> 12, r = (i >> 6) & 63, c = i & 63;
-    float m = 0.f;
-    if (c < r && r < nval) m = (S.raw[r][c] * fast_exp2(S.g[v][r] - S.g[v][c])) * S.beta[v][r];
-    S.m[v][r][c] = m;
-  }
-  __syncthreads();
-
-  // ---- phase 4: (I + M) X = I by forward substitution, one column j per thread: x_j = 1, x_r = 0 for r < j,
+  // ---- phase 3: (I + M) X = I by forward substitution, one column j per thread: x_j = 1, x_r = 0 for r < j,
   // x_r = -sum_{c<r} M[r][c] x_c for r > j (the terms with c < j vanish)
   if (tid < 2 * KKT_BT) {
     const int v = tid >> 6, j = tid & 63;
     const float(*M)[KKT_LDM] = S.m[v];
+    // entry (r, j) goes to A row r (stride HV * 64 elements) for r < nval and j up to the end of row r's own
+    // 16-column block; later columns are left untouched
+    uint16_t* dst = A + ((bos + t0) * HV + 2 * kh + v) * KKT_BT + j;
+    const long long rs = (long long)HV * KKT_BT;
     float x[KKT_BT];
 #pragma unroll
     for (int r = 0; r < KKT_BT; ++r) {
@@ -130,19 +122,8 @@ __global__ void __launch_bounds__(KKT_THREADS) kkt_kernel(const uint16_t* __rest
       for (int c = r & ~3; c < r; ++c) s0 = __builtin_fmaf(M[r][c], x[c], s0);
       const float s = (s0 + s1) + (s2 + s3);
       x[r] = r < j ? 0.f : r == j ? 1.f : 0.f - s;  // 0 - s: an exact zero is stored as +0
+      if (r < nval && j < 16 * (r / 16 + 1)) dst[r * rs] = bf16_bits(x[r]);
     }
-#pragma unroll
-    for (int r = 0; r < KKT_BT; ++r) S.x[v][r][j] = x[r];
-  }
-  __syncthreads();
-
-  // ---- phase 5: rows r < nval, columns up to the end of the row's 16-column block, as bf16 pairs
-  for (int i = tid; i < 2 * KKT_BT * (KKT_BT / 2); i += KKT_THREADS) {
-    const int v = i >> 11, r = (i >> 5) & 63, c2 = (i & 31) * 2;
-    if (r >= nval || c2 >= 16 * (r / 16 + 1)) continue;
-    const int hv = 2 * kh + v;
-    *reinterpret_cast<uint32_t*>(A + ((bos + t0 + r) * HV + hv) * KKT_BT + c2) =
-        pack_bf16x2(S.x[v][r][c2], S.x[v][r][c2 + 1]);
   }
 }
 
