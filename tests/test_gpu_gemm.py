@@ -36,7 +36,8 @@ def _close(got, ref, ulps, floor_rel):
 
 
 @pytest.mark.parametrize("M,N,K,ldd,cfg", [(64, 64, 64, 64, 0), (300, 520, 1024, 520, 7), (8, 4096, 2560, 4104, 14),
-                                           (1000, 136, 8, 144, 3)])
+                                           (1000, 136, 8, 144, 3), (1, 8, 8, 8, 2), (1, 8, 8, 8, 0),
+                                           (257, 264, 8200, 264, 1)])
 def test_plain_gemm(M, N, K, ldd, cfg):
     from reax_fmha import abi
 
@@ -87,7 +88,7 @@ def test_configs_bit_identical(lib):
 
 @pytest.mark.parametrize("part_fp32", [1, 0])
 @pytest.mark.parametrize("M,N,kps,S,K", [(64, 128, 256, 4, 1024), (200, 72, 64, 3, 200), (64, 128, 64, 2, 128),
-                                          (130, 256, 520, 1, 520)])
+                                          (130, 256, 520, 1, 520), (1, 8, 8, 1, 8), (33, 40, 8, 16, 128)])
 def test_slices(M, N, kps, S, K, part_fp32):
     from reax_fmha import abi
 
@@ -109,7 +110,7 @@ def test_slices(M, N, kps, S, K, part_fp32):
 
 
 @pytest.mark.parametrize("M,N2,K,cfg", [(128, 64, 256, 0), (77, 100, 520, 1), (512, 1024, 2560, 2), (300, 260, 64, 3),
-                                        (130, 516, 136, 0)])
+                                        (130, 516, 136, 0), (1, 4, 8, 2), (1, 4, 8, 16), (513, 132, 4104, 16)])
 def test_gv(M, N2, K, cfg):
     from reax_fmha import abi
 
