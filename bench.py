@@ -316,11 +316,12 @@ def bench_gemm(torch, ops, iters=20):
     d = torch.empty((M, Hd), dtype=torch.bfloat16, device="cuda")
     p = torch.empty((S, M, Hd), dtype=torch.float32, device="cuda")
     out = {}
-    # config indices covering the four tiles (128x128, 256x128, 128x256, 256x256) of each library
-    legs = [("gv", (2, 1, 0, 16), lambda c: ops.gv(x, wg, cfg=c, out=act), 2 * M * 2 * I * Hd,
+    # config indices 0-3 select the four LDS-ring tiles (256x256, 256x128, 128x128, 128x256) in each library
+    legs = [("gv", (0, 1, 2, 3), lambda c: ops.gv(x, wg, cfg=c, out=act), 2 * M * 2 * I * Hd,
              lambda: torch.matmul(x, wg.t())),
-            ("plain", (2, 1, 0), lambda c: ops.gemm(h, wd, cfg=c, d=d), 2 * M * Hd * I, lambda: torch.matmul(h, wd.t())),
-            ("slices", (2, 1, 0), lambda c: ops.slices(h, wd, kps=I // S, S=S, cfg=c, p=p), 2 * M * Hd * I, None)]
+            ("plain", (0, 1, 2, 3), lambda c: ops.gemm(h, wd, cfg=c, d=d), 2 * M * Hd * I,
+             lambda: torch.matmul(h, wd.t())),
+            ("slices", (0, 1, 2, 3), lambda c: ops.slices(h, wd, kps=I // S, S=S, cfg=c, p=p), 2 * M * Hd * I, None)]
     for name, cfgs, run, flops, ref in legs:
         best = min((_time_ms(torch, lambda: run(c), iters), c) for c in cfgs)
         tf = flops / (best[0] * 1e-3) / 1e12

@@ -9,8 +9,8 @@
 // that definition (an fp32 fast path with a double-precision fallback at bf16 rounding boundaries; the reference's
 // expf is accurate to about an ulp, so its bf16 SiLU can differ by one ulp in rare elements).
 //
-// Kernel: the shared matrix-core tiles (gemm_tile.h: 128 x 128 up to 256 x 256 tiles of C, K in slices of 64, the
-// config index picks the tile) with an epilogue that
+// Kernel: the shared matrix-core tiles (gemm_tile.h: 128 x 128 up to 256 x 256 tiles of C, K in slices of 64 copied
+// straight into an LDS ring, the config index picks the tile) with an epilogue that
 // pairs each gate column with the up column four to its right (four lanes over in the accumulator layout) and writes
 // only the activations: no intermediate buffer, like the reference's visitor.
 #include <hip/hip_runtime.h>
@@ -94,15 +94,13 @@ int launch_tile(const void* x, const void* w, void* out, int M, int N2, int K, v
 
 extern "C" {
 
-// tile of each config: the reference's threadblock shapes (gv:186-205) 128x256, 256x128, 128x128, 128x256, 128x256,
-// 256x128, 128x128, 128x128, 64x256, 128x256, 128x192, 128x192, 192x128, 192x128, 64x256, 64x256, 192x192, 128x128,
-// 128x128, 256x128, rounded to a gfx950 tile
-static const unsigned char kGvTile[20] = {2, 1, 0, 2, 2, 1, 0, 0, 2, 2, 2, 2, 1, 1, 2, 2, 3, 0, 0, 1};
-static const char* const kGvTileName[4] = {"mfma 128x128x64 4 waves", "mfma 256x128x64 8 waves",
-                                           "mfma 128x256x64 8 waves", "mfma 256x256x64 8 waves"};
+// tile of each config: 0 the 256 x 256 ring tile; the others by the reference's threadblock shapes (gv:186-205)
+// 256x128, 128x128, 128x256, 128x256, 256x128, 128x128, 128x128, 64x256, 128x256, 128x192, 128x192, 192x128, 192x128,
+// 64x256, 64x256, 192x192, 128x128, 128x128 (warp 64x32), 256x128
+static const unsigned char kGvTile[20] = {4, 2, 1, 3, 3, 2, 1, 1, 3, 3, 3, 3, 2, 2, 3, 3, 4, 1, 0, 2};
 
 int reax_gv_ncfg(void) { return 20; }
-const char* reax_gv_cfgname(int c) { return (c >= 0 && c < 20) ? kGvTileName[kGvTile[c]] : "?"; }
+const char* reax_gv_cfgname(int c) { return (c >= 0 && c < 20) ? reax::gemm::kTileNames[kGvTile[c]] : "?"; }
 
 int reax_gv(int cfg, const void* x, const void* w, void* out, int M, int N2, int K, void* stream) {
   if (cfg < 0 || cfg >= 20) return 9;  // gv:207
@@ -113,10 +111,12 @@ int reax_gv(int cfg, const void* x, const void* w, void* out, int M, int N2, int
       (reinterpret_cast<uintptr_t>(w) & 15u) || (reinterpret_cast<uintptr_t>(out) & 1u))
     return 3;
   using namespace reax::gemm;
-  switch (kGvTile[cfg]) {
-    case kT256x128: return reax::launch_tile<T256x128>(x, w, out, M, N2, K, stream);
-    case kT128x256: return reax::launch_tile<T128x256>(x, w, out, M, N2, K, stream);
-    case kT256x256: return reax::launch_tile<T256x256>(x, w, out, M, N2, K, stream);
+  const int tile = K % BK ? kT128x128 : kGvTile[cfg];  // the ring tiles copy whole 64-deep slices only
+  switch (tile) {
+    case kD128x128: return reax::launch_tile<D128x128>(x, w, out, M, N2, K, stream);
+    case kD256x128: return reax::launch_tile<D256x128>(x, w, out, M, N2, K, stream);
+    case kD128x256: return reax::launch_tile<D128x256>(x, w, out, M, N2, K, stream);
+    case kD256x256: return reax::launch_tile<D256x256>(x, w, out, M, N2, K, stream);
     default: return reax::launch_tile<T128x128>(x, w, out, M, N2, K, stream);
   }
 }

@@ -8,9 +8,10 @@
 //           bf16 or fp32 (part_fp32)
 //
 // The reference selects one of 15 / 16 CUTLASS sm80 tile configurations by index, all with the same results; here
-// index c runs the gfx950 tile (gemm_tile.h) nearest to the threadblock shape of the reference's config c, and all
-// tiles give the same bits too, so a caller that times every index and keeps the fastest still chooses among real
-// alternatives. An unknown index returns 9, as in the reference.
+// index 0 runs the tile that is fastest on large products (256 x 256) and index c > 0 the gfx950 tile (gemm_tile.h)
+// nearest to the threadblock shape of the reference's config c. All tiles give the same bits too, so a caller that
+// times every index and keeps the fastest still chooses among real alternatives. An unknown index returns 9, as in
+// the reference.
 // Shapes follow CUTLASS's can_implement for 8-wide bf16 accesses (code 1): positive sizes, K (kps) and the output
 // row stride multiples of 8; missing buffers and rows not 16-byte aligned also return 1 (the reference faults on
 // them). A failed launch returns 4, like the reference's trailing launch-error check.
@@ -77,17 +78,15 @@ int launch_tile(const void* x, const void* w, void* out, int M, int N, int K, in
 template <typename OutT>
 int launch(int tile, const void* x, const void* w, void* out, int M, int N, int K, int kext, int S, long long ldo,
            long long obs, void* stream) {
+  if (kext % gemm::BK) tile = gemm::kT128x128;  // the ring tiles copy whole 64-deep slices only
   switch (tile) {
-    case gemm::kT256x128: return launch_tile<gemm::T256x128, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
-    case gemm::kT128x256: return launch_tile<gemm::T128x256, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
-    case gemm::kT256x256: return launch_tile<gemm::T256x256, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
+    case gemm::kD128x128: return launch_tile<gemm::D128x128, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
+    case gemm::kD256x128: return launch_tile<gemm::D256x128, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
+    case gemm::kD128x256: return launch_tile<gemm::D128x256, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
+    case gemm::kD256x256: return launch_tile<gemm::D256x256, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
     default: return launch_tile<gemm::T128x128, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
   }
 }
-
-// names of the tiles, by id
-const char* const kTileName[4] = {"mfma 128x128x64 4 waves", "mfma 256x128x64 8 waves", "mfma 128x256x64 8 waves",
-                                  "mfma 256x256x64 8 waves"};
 
 }  // namespace
 }  // namespace reax
@@ -95,12 +94,13 @@ const char* const kTileName[4] = {"mfma 128x128x64 4 waves", "mfma 256x128x64 8 
 extern "C" {
 
 #if defined(REAX_LIB_PLAIN)
-// tile of each config: the reference's threadblock shapes (gemm_plain2.cu:40-54) 128x256, 256x128, 128x128, 128x256,
-// 128x256, 192x128, 192x128, 64x256, 64x256, 128x128, 128x128, 256x128, 256x64, 128x64, 64x128, rounded to a gfx950 tile
-static const unsigned char kPlainTile[15] = {2, 1, 0, 2, 2, 1, 1, 2, 2, 0, 0, 1, 1, 0, 0};
+// tile of each config: 0 the 256 x 256 ring tile; the others by the reference's threadblock shapes
+// (gemm_plain2.cu:40-54) 256x128, 128x128, 128x256, 128x256, 192x128, 192x128, 64x256, 64x256, 128x128, 128x128
+// (warp 64x32), 256x128, 256x64, 128x64, 64x128
+static const unsigned char kPlainTile[15] = {4, 2, 1, 3, 3, 2, 2, 3, 3, 1, 0, 2, 2, 1, 0};
 
 int reax_gemm_ncfg(void) { return 15; }
-const char* reax_gemm_cfgname(int c) { return (c >= 0 && c < 15) ? reax::kTileName[kPlainTile[c]] : "?"; }
+const char* reax_gemm_cfgname(int c) { return (c >= 0 && c < 15) ? reax::gemm::kTileNames[kPlainTile[c]] : "?"; }
 
 int reax_gemm(int cfg, const void* x, const void* w, void* d, int M, int N, int K, int ldd, void* stream) {
   if (cfg < 0 || cfg >= 15) return 9;  // gemm_plain2.cu:56
@@ -111,13 +111,13 @@ int reax_gemm(int cfg, const void* x, const void* w, void* d, int M, int N, int 
 }
 
 #else
-// tile of each config: the reference's threadblock shapes (gemm_slices_v2.cu:38-53) 128x256, 256x128, 128x128,
-// 64x256, 128x128, 256x128, 128x256, 64x128, 128x64, 64x256, 64x128, 256x64, 128x128, 128x128, 64x128, 256x128,
-// rounded to a gfx950 tile
-static const unsigned char kSlicesTile[16] = {2, 1, 0, 2, 0, 1, 2, 0, 0, 2, 0, 1, 0, 0, 0, 1};
+// tile of each config: 0 the 256 x 256 ring tile; the others by the reference's threadblock shapes
+// (gemm_slices_v2.cu:38-53) 256x128, 128x128, 64x256, 128x128, 256x128, 128x256, 64x128, 128x64, 64x256, 64x128,
+// 256x64, 128x128, 128x128, 64x128, 256x128
+static const unsigned char kSlicesTile[16] = {4, 2, 1, 3, 1, 2, 3, 0, 1, 3, 0, 2, 1, 1, 0, 2};
 
 int reax_slices_ncfg(void) { return 16; }
-const char* reax_slices_cfgname(int c) { return (c >= 0 && c < 16) ? reax::kTileName[kSlicesTile[c]] : "?"; }
+const char* reax_slices_cfgname(int c) { return (c >= 0 && c < 16) ? reax::gemm::kTileNames[kSlicesTile[c]] : "?"; }
 
 int reax_slices(int cfg, int part_fp32, const void* x, const void* w, void* p, int M, int N, int kps, int S, int K,
                 void* stream) {

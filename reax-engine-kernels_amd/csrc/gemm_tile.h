@@ -5,9 +5,9 @@
 // A tile is NWM x NWN wavefronts, each a (32 WTM) x (32 WTN) block of C as WTM x WTN v_mfma_f32_32x32x16_bf16
 // tiles, so that one 16-deep step reads WTM + WTN fragments for WTM * WTN MFMAs (larger wave blocks need less LDS
 // bandwidth per MFMA). K advances 64 at a time: the BM x 64 and BN x 64 slices of X and W live in LDS (16-byte units
-// XOR-swizzled by row, so every MFMA fragment is one conflict-free 16-byte read), double-buffered, and the next
-// slice is read from global memory into registers while the current one is multiplied (one barrier per slice). Rows
-// beyond M or N and k units at or beyond k1 read as zeros; k0 and k1 are multiples of 8 (whole 16-byte units).
+// XOR-swizzled by row, so every MFMA fragment is one conflict-free 16-byte read), one barrier per slice. Tile stages
+// a slice through registers (read while the previous slice is multiplied; rows beyond M or N and k units at or
+// beyond k1 read as zeros; k0 and k1 multiples of 8); DmaTile copies slices straight into an LDS ring (below).
 //
 // Every tile shape adds each accumulator's K slices in the same ascending order of 16-element MFMA steps, so all
 // shapes give identical bits; against another summation order results agree to fp32 accumulation accuracy.
@@ -123,14 +123,115 @@ struct Tile {
   }
 };
 
-// The tile shapes a config index can select. 128 x 128 runs 4 wavefronts of 64 x 64 (two workgroups per CU, 64 KB
-// LDS each); the larger tiles run 8 wavefronts (one workgroup per CU, 96 or 128 KB LDS), which halves (256 x 256)
-// or cuts by a quarter the operand bytes per MFMA read through L2.
-using T128x128 = Tile<2, 2, 2, 2>;
-using T256x128 = Tile<4, 2, 2, 2>;
-using T128x256 = Tile<2, 4, 2, 2>;
-using T256x256 = Tile<2, 4, 4, 2>;
-enum TileId : unsigned char { kT128x128 = 0, kT256x128 = 1, kT128x256 = 2, kT256x256 = 3 };
+// The same tile with the K slices copied straight from global memory into LDS (global_load_lds_dwordx4, no
+// register staging) through a ring of NS slices, NS - 1 slices ahead of the multiply. The copy of a 1 KB chunk
+// (8 rows of a 64-wide slice) puts lane l's 16 bytes at chunk + 16 l, so lane l fetches the unit that the XOR
+// swizzle places there: row 8 c + l / 8, unit (l % 8) ^ (row % 8). The copies are issued as inline assembly, which
+// the compiler does not track: each wavefront waits for its own copies with s_waitcnt vmcnt (they complete in issue
+// order) and the barrier that follows makes every wavefront's copies visible. Rows beyond M or N read the last
+// valid row (their outputs are never stored); the K extent must be a whole number of slices (no zero fill).
+template <int NWM_, int NWN_, int WTM_, int WTN_, int NS_>
+struct DmaTile {
+  static constexpr int NWM = NWM_, NWN = NWN_, WTM = WTM_, WTN = WTN_, NS = NS_;
+  static constexpr int THREADS = 64 * NWM * NWN, NWAVES = NWM * NWN;
+  static constexpr int BM = 32 * WTM * NWM, BN = 32 * WTN * NWN;
+  static constexpr int XCH = BM / 8, CH = (BM + BN) / 8;  // 1 KB chunks of X, of the whole slice
+  static constexpr int CPW = CH / NWAVES;                  // chunks copied per wavefront per slice
+  static_assert(CPW * NWAVES == CH, "whole chunks per wavefront");
+  static_assert(NS == 2 || NS == 3, "two or three slices in the ring");
+
+  struct Lds {
+    uint16_t xs[NS][BM * BK];
+    uint16_t ws[NS][BN * BK];
+  };
+  using Acc = f32x16_t[WTM][WTN];
+
+  __device__ static int wm() { return 32 * WTM * ((int)(threadIdx.x >> 6) / NWN); }
+  __device__ static int wn() { return 32 * WTN * ((int)(threadIdx.x >> 6) % NWN); }
+
+  __device__ __forceinline__ static void mainloop(Lds& S, const uint16_t* __restrict__ x,
+                                                  const uint16_t* __restrict__ w, long long ldx, int k0, int k1,
+                                                  int M, int N, int m_blk, int n_blk, Acc& acc) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm0 = wm(), wn0 = wn();
+    // copy slice kb into ring slot st: chunks wv * CPW .. wv * CPW + CPW - 1
+    auto copy = [&](int st, int kb) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < CPW; ++i) {
+        const int c = wv * CPW + i;
+        const bool isx = c < XCH;
+        const int r = 8 * (isx ? c : c - XCH) + (lane >> 3);
+        const int u = (lane & 7) ^ (r & 7);
+        const int row = isx ? min(m_blk + r, M - 1) : min(n_blk + r, N - 1);
+        const uint16_t* src = (isx ? x : w) + (long long)row * ldx + kb + 8 * u;
+        const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+            (uint32_t)reinterpret_cast<uintptr_t>(isx ? &S.xs[st][c * 512] : &S.ws[st][(c - XCH) * 512]));
+        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+      }
+    };
+    auto compute = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        const int u = 2 * ks + (lane >> 5), r = lane & 31;
+        bf16x8_t af[WTM], bf[WTN];
+#pragma unroll
+        for (int a = 0; a < WTM; ++a)
+          af[a] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&S.xs[st][slot(wm0 + 32 * a + r, u)]));
+#pragma unroll
+        for (int b = 0; b < WTN; ++b)
+          bf[b] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&S.ws[st][slot(wn0 + 32 * b + r, u)]));
+#pragma unroll
+        for (int a = 0; a < WTM; ++a)
+#pragma unroll
+          for (int b = 0; b < WTN; ++b) acc[a][b] = mfma32(af[a], bf[b], acc[a][b]);
+      }
+    };
+#pragma unroll
+    for (int a = 0; a < WTM; ++a)
+#pragma unroll
+      for (int b = 0; b < WTN; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+
+    const int nk = (k1 - k0) / BK;
+    // prologue: slices 0 .. NS - 2 in flight; wait for slice 0
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j)
+      if (j < nk) copy(j, k0 + j * BK);
+    if (NS == 2 || nk == 1)
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(CPW));  // slice 1's copies may still be in flight
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      // slot (kt + NS - 1) % NS was last read in step kt - 1, before its closing barrier
+      if (kt + NS - 1 < nk) copy((kt + NS - 1) % NS, k0 + (kt + NS - 1) * BK);
+      compute(kt % NS);
+      if (kt + 1 < nk) {
+        // slice kt + 1 must have landed; slice kt + 2 (NS = 3, if there is one: CPW copies) may still be in flight
+        if (NS == 3 && kt + 2 < nk)
+          __builtin_amdgcn_s_waitcnt(vmcnt_le(CPW));
+        else
+          __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+        __syncthreads();
+      }
+    }
+  }
+};
+
+// The tiles a config index can select (measured at the MLP shapes of the GEMM bench leg: the 8-wavefront 256 x 256
+// ring tile is the fastest there; 3-slice rings, which fit one workgroup per CU, and 4-wavefront 256 x 256 tiles,
+// which spill, were slower). Register staging remains for K extents that are not whole slices.
+using T128x128 = Tile<2, 2, 2, 2>;            // 4 wavefronts, register-staged, 64 KB LDS (two workgroups per CU)
+using D128x128 = DmaTile<2, 2, 2, 2, 2>;      // 4 wavefronts, 64 KB
+using D256x128 = DmaTile<4, 2, 2, 2, 2>;      // 8 wavefronts of 64 x 64, 96 KB
+using D128x256 = DmaTile<2, 4, 2, 2, 2>;      // 8 wavefronts of 64 x 64, 96 KB
+using D256x256 = DmaTile<2, 4, 4, 2, 2>;      // 8 wavefronts of 128 x 64, 128 KB
+enum TileId : unsigned char { kT128x128 = 0, kD128x128 = 1, kD256x128 = 2, kD128x256 = 3, kD256x256 = 4 };
+constexpr const char* kTileNames[5] = {"mfma 128x128x64, 4 waves, register-staged", "mfma 128x128x64, 4 waves, LDS ring",
+                                       "mfma 256x128x64, 8 waves, LDS ring", "mfma 128x256x64, 8 waves, LDS ring",
+                                       "mfma 256x256x64, 8 waves, LDS ring"};
 
 // XCD-aware tile order: hardware hands consecutive workgroups to the 8 XCDs in turn, so workgroup b runs on XCD
 // b % 8. When the tile count is a multiple of 8, each XCD is given a contiguous range of the tile sequence; the

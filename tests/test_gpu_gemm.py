@@ -56,20 +56,21 @@ def test_plain_gemm(M, N, K, ldd, cfg):
     assert bad == 0, f"{bad} outputs off (max error {rel:.3g} of the scale)"
 
 
+@pytest.mark.parametrize("K", [392, 512])
 @pytest.mark.parametrize("lib", ["plain", "slices", "gv"])
-def test_configs_bit_identical(lib):
+def test_configs_bit_identical(lib, K):
     """Every config index (tile shape) adds each output's K terms in the same order: identical bits (the reference's
     configs share one reduction order too, gemm_slices_v2.cu:5-8)."""
     from reax_fmha import abi
 
-    M, N, K = 300, 264, 392
+    M, N = 300, 264  # K = 512: whole 64-deep slices, so the direct-to-LDS tiles run too
     x, w = _rand((M, K), 7), _rand((N, K), 8, 0.1)
     dx, dw = W.bits_to_torch(x, "cuda"), W.bits_to_torch(w, "cuda")
     st = torch.cuda.current_stream().cuda_stream
     outs = []
     ncfg = {"plain": 15, "slices": 16, "gv": 20}[lib]
     for cfg in range(ncfg):
-        _say(f"{lib} cfg={cfg}")
+        _say(f"{lib} K={K} cfg={cfg}")
         if lib == "plain":
             o = torch.zeros((M, N), dtype=torch.bfloat16, device="cuda")
             rc = abi.plain().reax_gemm(cfg, dx.data_ptr(), dw.data_ptr(), o.data_ptr(), M, N, K, N, st)
