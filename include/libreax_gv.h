@@ -10,7 +10,9 @@ extern "C" {
 
 /* Number of config indices reax_gv accepts (20, as gateup_vis2.cu:172). */
 int reax_gv_ncfg(void);
-/* Name of config c, "?" outside 0..19 (gateup_vis2.cu:173-181); here every index runs the same kernel. */
+/* Name of config c, "?" outside 0..19 (gateup_vis2.cu:173-181); the index selects one of the
+ * gfx950 matrix-core tiles (index 0: 256 x 256; the others the tile nearest the reference config's shape), which the
+ * name describes. All give identical bits. */
 const char* reax_gv_cfgname(int c);
 /* out[M][N2] = bf16(bf16(silu(bf16(g))) * bf16(u)) with [g | u] = X[M][K] W[2*N2][K]^T, W's rows interleaving 4 gate
  * and 4 up rows per group of 4 output features (gateup_vis2.cu:1-6); replaces reax_gv, gateup_vis2.cu:182-208.

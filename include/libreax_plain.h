@@ -11,8 +11,8 @@ extern "C" {
 /* Number of config indices reax_gemm accepts (15, as gemm_plain2.cu:31). */
 int reax_gemm_ncfg(void);
 /* Name of config c, "?" outside 0..14 (gemm_plain2.cu:32-36). The index selects a CUTLASS tile shape in the
- * reference (all with the same results); here every index runs the one gfx950 MFMA tile, so the names only number
- * the indices. */
+ * reference (all with the same results); here it selects one of the gfx950 matrix-core tiles (index 0: 256 x 256;
+ * the others the tile nearest the reference config's shape), which the name describes. All give identical bits. */
 const char* reax_gemm_cfgname(int c);
 /* D[M][N] (row stride ldd) = bf16(X[M][K] W[N][K]^T) with fp32 accumulation; replaces reax_gemm, gemm_plain2.cu:37-56.
  * Returns 0 on success, 9 for an unknown cfg (as the reference), 1 for shapes the reference's kernels cannot take

@@ -10,8 +10,9 @@ extern "C" {
 
 /* Number of config indices reax_slices accepts (16, as gemm_slices_v2.cu:56). */
 int reax_slices_ncfg(void);
-/* Name of config c, "?" outside 0..15 (gemm_slices_v2.cu:57-64); here every index runs the one gfx950
- * MFMA tile. */
+/* Name of config c, "?" outside 0..15 (gemm_slices_v2.cu:57-64); the index selects one of the gfx950
+ * matrix-core tiles (index 0: 256 x 256; the others the tile nearest the reference config's shape), which the name
+ * describes. All give identical bits. */
 const char* reax_slices_cfgname(int c);
 /* Split-K partials: for s = 0..S-1, P[s][M][N] = X[:, s*kps .. (s+1)*kps) W[:, s*kps .. (s+1)*kps)^T with X [M][K]
  * and W [N][K] row-major, fp32 accumulation, each partial rounded once to fp32 (part_fp32 != 0) or bf16, partial s at
