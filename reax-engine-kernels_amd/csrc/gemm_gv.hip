@@ -82,7 +82,8 @@ __global__ void __launch_bounds__(T::THREADS) gv_kernel(const uint16_t* __restri
 
 template <class T>
 int launch_tile(const void* x, const void* w, void* out, int M, int N2, int K, void* stream) {
-  const int tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (2 * N2 + T::BN - 1) / T::BN;
+  const int tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (int)((2LL * N2 + T::BN - 1) / T::BN);
+  if ((long long)tiles_m * tiles_n > INT32_MAX) return 3;  // more tiles than one grid dimension holds
   hipLaunchKernelGGL(gv_kernel<T>, dim3((unsigned)(tiles_m * tiles_n)), dim3(T::THREADS), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
                      static_cast<uint16_t*>(out), M, N2, K, tiles_m, tiles_n);
@@ -105,9 +106,10 @@ const char* reax_gv_cfgname(int c) { return (c >= 0 && c < 20) ? reax::gemm::kTi
 int reax_gv(int cfg, const void* x, const void* w, void* out, int M, int N2, int K, void* stream) {
   if (cfg < 0 || cfg >= 20) return 9;  // gv:207
   if (K % 8 || N2 % 4) return 1;       // gv:143
-  // empty or negative sizes, missing or misaligned buffers (16-byte row loads): the reference's kernel cannot take
-  // them either (an empty grid fails to launch, misaligned loads fault)
-  if (M <= 0 || N2 <= 0 || K <= 0 || !x || !w || !out || (reinterpret_cast<uintptr_t>(x) & 15u) ||
+  // empty or negative sizes, 2 N2 beyond int, missing or misaligned buffers (16-byte row loads): the reference's
+  // kernel cannot take them either (an empty grid fails to launch, its int problem size overflows, misaligned loads
+  // fault)
+  if (M <= 0 || N2 <= 0 || N2 > INT32_MAX / 2 || K <= 0 || !x || !w || !out || (reinterpret_cast<uintptr_t>(x) & 15u) ||
       (reinterpret_cast<uintptr_t>(w) & 15u) || (reinterpret_cast<uintptr_t>(out) & 1u))
     return 3;
   using namespace reax::gemm;

@@ -69,6 +69,7 @@ template <class T, typename OutT>
 int launch_tile(const void* x, const void* w, void* out, int M, int N, int K, int kext, int S, long long ldo,
                 long long obs, void* stream) {
   const int tiles_m = (M + T::BM - 1) / T::BM, tiles_n = (N + T::BN - 1) / T::BN;
+  if ((long long)tiles_m * tiles_n > INT32_MAX) return 4;  // more tiles than one grid dimension holds
   hipLaunchKernelGGL((gemm_kernel<T, OutT>), dim3((unsigned)(tiles_m * tiles_n), 1, (unsigned)S), dim3(T::THREADS), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(w),
                      static_cast<OutT*>(out), M, N, K, kext, ldo, obs, tiles_m, tiles_n);

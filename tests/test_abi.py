@@ -137,6 +137,7 @@ def test_gemm_argument_codes():
     assert G.reax_gv(0, None, None, None, 8, 8, 12, None) == 1              # K % 8
     assert G.reax_gv(0, None, None, None, 8, 6, 8, None) == 1               # N2 % 4
     assert G.reax_gv(0, None, None, None, 0, 8, 8, None) == 3               # empty grid
+    assert G.reax_gv(0, None, None, None, 8, 2 ** 30 + 4, 8, None) == 3     # 2 N2 beyond int
 
 
 def test_splitkv_workspace_size():
