@@ -133,3 +133,33 @@ def test_gv(M, N2, K, cfg):
     assert np.isfinite(got).all(), "an activation left unwritten"
     bad, rel = _close(got, ref, 2, 2.0 ** -12)
     assert bad == 0, f"{bad} activations off (max error {rel:.3g} of the scale)"
+
+
+@pytest.mark.parametrize("lib", ["plain", "gv"])
+def test_offset_bases(lib):
+    """X and W starting 16 bytes into their allocations (the ABI asks for 16-byte alignment only): same bits as the
+    aligned call, on a whole-slice K (the direct-to-LDS tiles) and a ragged one (register-staged)."""
+    from reax_fmha import abi
+
+    st = torch.cuda.current_stream().cuda_stream
+    for K in (512, 200):
+        M, N = 136, 264
+        _say(f"{lib} offset bases K={K}")
+        x, w = _rand((M, K), 11), _rand((N, K), 12, 0.1)
+        dx, dw = W.bits_to_torch(x, "cuda"), W.bits_to_torch(w, "cuda")
+        bx = torch.zeros(M * K + 8, dtype=torch.bfloat16, device="cuda")
+        bw = torch.zeros(N * K + 8, dtype=torch.bfloat16, device="cuda")
+        bx[8:] = dx.reshape(-1)
+        bw[8:] = dw.reshape(-1)
+        outs = []
+        for px, pw in ((dx.data_ptr(), dw.data_ptr()), (bx.data_ptr() + 16, bw.data_ptr() + 16)):
+            if lib == "plain":
+                o = torch.zeros((M, N), dtype=torch.bfloat16, device="cuda")
+                rc = abi.plain().reax_gemm(0, px, pw, o.data_ptr(), M, N, K, N, st)
+            else:
+                o = torch.zeros((M, N // 2), dtype=torch.bfloat16, device="cuda")
+                rc = abi.gv().reax_gv(0, px, pw, o.data_ptr(), M, N // 2, K, st)
+            torch.cuda.synchronize()
+            assert rc == 0
+            outs.append(o.view(torch.int16).cpu().numpy())
+        assert np.array_equal(outs[0], outs[1]), f"K={K}: offset bases change the result"
