@@ -1,6 +1,6 @@
 // libreax_plain.so (-DREAX_LIB_PLAIN) and libreax_slices.so (-DREAX_LIB_SLICES) for MI355X: the plain and split-K
 // ("slices") bf16 GEMMs behind their config-index C ABIs (libreax_plain/gemm_plain2.cu:31-57,
-// libreax_slices/gemm_slices_v2.cu:55-84), on the shared matrix-core tile (gemm_tile.h: fp32 accumulation in
+// libreax_slices/gemm_slices_v2.cu:55-84), on the shared matrix-core tiles (gemm_tile.h: fp32 accumulation in
 // ascending K, each output rounded once to its storage type).
 //
 //   plain:  D[m][n] = X[m][:] . W[n][:]                  X [M][K], W [N][K] row-major, D row stride ldd
