@@ -148,3 +148,15 @@ def test_splitkv_workspace_size():
     assert L.reax_fmha_splitkv_workspace(16, 8, 4, 128, 16) == want
     assert L.reax_fmha_splitkv_workspace(16, 8, 4, 64, 16) == 0  # unsupported head_dim
     assert L.reax_fmha_splitkv_workspace(16, 8, 4, 128, 0) == 0
+
+
+def test_gemm_config_names_cover_the_tiles():
+    # every index names one of the gfx950 tiles; index 0 is the 256 x 256 ring tile in each library, and every tile
+    # is reachable from some index of each library (so a caller that times all indices tries each tile)
+    P, S, G = abi.plain(), abi.slices(), abi.gv()
+    for name, fn, n in (("plain", P.reax_gemm_cfgname, 15), ("slices", S.reax_slices_cfgname, 16),
+                        ("gv", G.reax_gv_cfgname, 20)):
+        names = [fn(c).decode() for c in range(n)]
+        assert all(x.startswith("mfma ") for x in names), (name, names)
+        assert names[0].startswith("mfma 256x256x64"), (name, names[0])
+        assert len(set(names)) == 5, (name, sorted(set(names)))
