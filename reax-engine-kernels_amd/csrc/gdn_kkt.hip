@@ -10,8 +10,8 @@
 // (v_exp_f32, full-precision forward substitution), so its results are at least as close to the exact inverse;
 // agreement with the reference is to its own tf32/bf16 accuracy, not bit for bit.
 //
-// Layout: one workgroup of 256 threads per (chunk, key head), 52 KB of LDS so that three workgroups share a CU and
-// one's solve overlaps the others' loads and products. Phase 1 stages the chunk's k (64 x 128 bf16, 16-byte units XOR-swizzled by row),
+// Layout: one workgroup of 256 threads per (chunk, key head), 34 KB of LDS (M packed as a triangle) so that four
+// workgroups share a CU and one's solve overlaps the others' loads and products. Phase 1 stages the chunk's k (64 x 128 bf16, 16-byte units XOR-swizzled by row),
 // g and beta; phase 2 forms k k^T with v_mfma_f32_32x32x16_bf16 (wavefronts 0-2: the two diagonal 32 x 32 tiles and
 // the one below them) and writes M for both value heads straight from the accumulators (decay, mask and beta);
 // phase 3 solves (I + M) X = I column by column (128 threads: 2 heads x 64 columns, the column in registers, M read
@@ -32,11 +32,17 @@ namespace {
 constexpr int KKT_BT = 64, KKT_K = 128, KKT_THREADS = 256;
 
 __device__ __forceinline__ uint16_t bf16_bits(float x) { return (uint16_t)(pack_bf16x2(x, 0.f) & 0xffffu); }
-constexpr int KKT_LDM = KKT_BT + 4;  // rows of M: 16-byte aligned, read 4 entries at a time by broadcast
+
+// Row r of M (columns 0 .. r-1, padded to a multiple of 4 so that every row starts 16-byte aligned for the
+// broadcast reads of the solve) starts at moff(r) floats: the strictly lower triangle in 2112 floats per head.
+__host__ __device__ constexpr int moff(int r) {
+  return r == 0 ? 0 : 4 * (2 * ((r - 1) / 4) * ((r - 1) / 4 + 1) + ((r - 1) % 4) * ((r - 1) / 4 + 1));
+}
+constexpr int KKT_MTRI = moff(KKT_BT);
 
 struct KktLds {
   uint16_t k[KKT_BT * KKT_K];  // k rows, 16-byte units XOR-swizzled by row
-  float m[2][KKT_BT][KKT_LDM];
+  float m[2][KKT_MTRI];        // M of each value head, packed rows
   float g[2][KKT_BT];
   float beta[2][KKT_BT];
 };
@@ -44,7 +50,7 @@ struct KktLds {
 // element (r, c) of the staged k: 16 units of 8 per row, unit index XOR row % 16
 __device__ __forceinline__ int ksw(int r, int c) { return r * KKT_K + ((((c >> 3) ^ (r & 15))) << 3) + (c & 7); }
 
-__global__ void __launch_bounds__(KKT_THREADS, 3) kkt_kernel(const uint16_t* __restrict__ k, const float* __restrict__ g,
+__global__ void __launch_bounds__(KKT_THREADS, 4) kkt_kernel(const uint16_t* __restrict__ k, const float* __restrict__ g,
                                                              const uint16_t* __restrict__ beta, uint16_t* __restrict__ A,
                                                              const int64_t* __restrict__ cu,
                                                              const int64_t* __restrict__ cidx, int H, int HV) {
@@ -89,10 +95,12 @@ __global__ void __launch_bounds__(KKT_THREADS, 3) kkt_kernel(const uint16_t* __r
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       const int r = 32 * I + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-      const bool live = c < r && r < nval;
+      if (c < r) {  // the solve reads only the strictly lower triangle
+        const bool live = r < nval;
 #pragma unroll
-      for (int v = 0; v < 2; ++v)
-        S.m[v][r][c] = live ? (acc[e] * fast_exp2(S.g[v][r] - S.g[v][c])) * S.beta[v][r] : 0.f;
+        for (int v = 0; v < 2; ++v)
+          S.m[v][moff(r) + c] = live ? (acc[e] * fast_exp2(S.g[v][r] - S.g[v][c])) * S.beta[v][r] : 0.f;
+      }
     }
   }
   __syncthreads();
@@ -101,7 +109,7 @@ __global__ void __launch_bounds__(KKT_THREADS, 3) kkt_kernel(const uint16_t* __r
   // x_r = -sum_{c<r} M[r][c] x_c for r > j (the terms with c < j vanish)
   if (tid < 2 * KKT_BT) {
     const int v = tid >> 6, j = tid & 63;
-    const float(*M)[KKT_LDM] = S.m[v];
+    const float* M = S.m[v];
     // entry (r, j) goes to A row r (stride HV * 64 elements) for r < nval and j up to the end of row r's own
     // 16-column block; later columns are left untouched
     uint16_t* dst = A + ((bos + t0) * HV + 2 * kh + v) * KKT_BT + j;
@@ -112,14 +120,14 @@ __global__ void __launch_bounds__(KKT_THREADS, 3) kkt_kernel(const uint16_t* __r
       float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
       for (int c = 0; c + 3 < r; c += 4) {
-        const f32x4_t mr = *reinterpret_cast<const f32x4_t*>(&M[r][c]);
+        const f32x4_t mr = *reinterpret_cast<const f32x4_t*>(&M[moff(r) + c]);
         s0 = __builtin_fmaf(mr[0], x[c], s0);
         s1 = __builtin_fmaf(mr[1], x[c + 1], s1);
         s2 = __builtin_fmaf(mr[2], x[c + 2], s2);
         s3 = __builtin_fmaf(mr[3], x[c + 3], s3);
       }
 #pragma unroll
-      for (int c = r & ~3; c < r; ++c) s0 = __builtin_fmaf(M[r][c], x[c], s0);
+      for (int c = r & ~3; c < r; ++c) s0 = __builtin_fmaf(M[moff(r) + c], x[c], s0);
       const float s = (s0 + s1) + (s2 + s3);
       x[r] = r < j ? 0.f : r == j ? 1.f : 0.f - s;  // 0 - s: an exact zero is stored as +0
       if (r < nval && j < 16 * (r / 16 + 1)) dst[r * rs] = bf16_bits(x[r]);
