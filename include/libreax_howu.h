@@ -108,8 +108,9 @@ int reax_conv_v(const void* qkv, long long SX, const void* cache, int C, const v
  * cidx[2n+1] = 64-token chunk of it; cu = int64 sequence starts) and key head kh, for value heads hv = 2kh, 2kh+1:
  * A = (I + M)^-1 with M[r][c] = (k_r . k_c) * 2^(g[r] - g[c]) * beta[r] for c < r within the chunk; k bf16
  * [T][H][128], g fp32 [T][HV], beta bf16 [T][HV], A bf16 [T][HV][64] (row r written up to the end of its 16-column
- * block; other entries untouched). Computed in fp32 (the reference uses bf16 / tf32 tensor-core products and an
- * approximate ex2: agreement with it is to that accuracy). Returns -1 for HV != 2H (the reference's code),
+ * block; other entries untouched). k . k^T runs on the bf16 matrix cores (exact products, fp32 accumulation); the
+ * decay, mask, beta and the forward substitution run in fp32 (the reference uses bf16 / tf32 tensor-core products
+ * and an approximate ex2: agreement with it is to that accuracy). Returns -1 for HV != 2H (the reference's code),
  * hipErrorInvalidConfiguration for NT or H <= 0 (an empty grid), hipErrorInvalidValue for missing or misaligned
  * buffers, else hipGetLastError(). */
 int reax_kkt(const void* k, const void* g, const void* beta, void* A, const void* cu, const void* cidx, int NT, int H,

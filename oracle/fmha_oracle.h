@@ -17,6 +17,10 @@
 //   - logits: x = (s*scale + bias_or_0) in natural-log units; the kernel works in base 2  (v8:266-288)
 //   - a row that sees no key, or whose visible logits are all -inf, outputs 0             (v8:303, v8:331-334)
 //   - qpos = 0: the row sees key 0 only, so O = V[0] exactly                              (v8:224-235)
+//   - drop-in block rule (reax_fmha_q / reax_fmha_qp only, Args::qpos0_block): folded rows of (b, h) form blocks
+//     [64j, 64j + 64); when the largest raw qpos over a block's rows is 0, every row of the block, qpos < 0 rows
+//     included, sees key 0 only and so stores V[0]                                        (v8:155-162, 224-235;
+//                                                                                        v11:213-220, 282-293)
 //   - POST: out[inv[b*Lq + r/G]][(h*G + r%G)*D + d] = bf16(bf16(o) * bf16(sigmoid(gate))), gate at +D in the
 //     [T][Hq][2D] qg tensor; inv < 0 rows are skipped                                       (v11:451-522, 583-590)
 // Extensions that the reference does not have (pinned only by this oracle and the tests that check it):
@@ -54,6 +58,7 @@ struct Args {
   int32_t key_lo, key_hi;  // keys outside [key_lo, key_hi) are invisible; key_hi <= 0 means "no upper window"
   int32_t p_bf16;          // 1: round P to bf16 before P.V (the GPU kernels do), the row sum keeps fp P
   float scale;
+  int32_t qpos0_block;     // 1: the drop-in entry points' block-wide qpos = 0 rule (see row_last_key)
 };
 
 // Deliberate mistakes that tests plant in the oracle (on the CPU) to show that the pins catch them.
@@ -67,6 +72,9 @@ enum Mutant : int32_t {
   MUT_SIGMOID_SIGN = 6,    // sigmoid(-x)
   MUT_GATE_QUERY_HALF = 7, // POST reads the query half of qg (offset 0) instead of the gate half (offset D)
   MUT_COMBINE_NO_WEIGHT = 8,  // split combine averages partial outputs instead of LSE-weighting them
+  MUT_BLOCK_TOKENS = 9,       // qpos = 0 block rule over blocks of 64 tokens instead of 64 folded rows
+  MUT_BLOCK_CLAMPED = 10,     // qpos = 0 block rule on qpos clamped to N - 1 instead of the raw qpos
+  MUT_BLOCK_OFF = 11,         // qpos = 0 block rule ignored (per-row rule only)
 };
 extern int32_t g_mutant;
 
@@ -136,11 +144,35 @@ inline BatchView batch_view(const Args& a, int b) {
   return BatchView{0, a.M, a.N};
 }
 
+// Largest qpos over the 64-row block of folded row r (reax_fmha_v8.cu:141-162: cta_qmax over the CTA's 64 rows,
+// rows at or beyond M count as -1). The reference compares the raw qpos, before any clamp to the key count.
+inline int64_t block_qpos_max(const Args& a, int b, int r, const BatchView& bv) {
+  const int64_t M = bv.rows;
+  int64_t lo, hi;  // row range [lo, hi) of the block
+  if (g_mutant == MUT_BLOCK_TOKENS) {
+    const int64_t t0 = (int64_t)(r / a.G) / 64 * 64;
+    lo = t0 * a.G;
+    hi = lo + 64LL * a.G;
+  } else {
+    lo = (int64_t)r / 64 * 64;
+    hi = lo + 64;
+  }
+  if (hi > M) hi = M;
+  int64_t mx = -1;
+  for (int64_t rr = lo; rr < hi; ++rr) {
+    int64_t qp = a.qpos[(int64_t)b * a.qpBs + rr / a.G];
+    if (g_mutant == MUT_BLOCK_CLAMPED && qp > bv.keys - 1) qp = bv.keys - 1;
+    if (qp > mx) mx = qp;
+  }
+  return mx;
+}
+
 // Last key index (inclusive) that row r may see before the key window, or -1.
 inline int64_t row_last_key(const Args& a, int b, int r, const BatchView& bv) {
   const int tok = r / a.G;
   switch (a.mask_mode) {
     case MASK_QPOS: {
+      if (a.qpos0_block && g_mutant != MUT_BLOCK_OFF && bv.keys > 0 && block_qpos_max(a, b, r, bv) == 0) return 0;
       const int64_t qp = a.qpos[(int64_t)b * a.qpBs + tok];
       if (qp < 0) return -1;
       const int64_t lim = g_mutant == MUT_CAUSAL_STRICT ? qp - 1 : qp;

@@ -28,6 +28,9 @@ MUTANTS = {
     "sigmoid_sign": 6,
     "gate_query_half": 7,
     "combine_no_weight": 8,
+    "block_tokens": 9,
+    "block_clamped": 10,
+    "block_off": 11,
 }
 
 
@@ -45,6 +48,7 @@ class Args(ctypes.Structure):
         ("M", ctypes.c_int32), ("N", ctypes.c_int32), ("D", ctypes.c_int32),
         ("key_lo", ctypes.c_int32), ("key_hi", ctypes.c_int32), ("p_bf16", ctypes.c_int32),
         ("scale", ctypes.c_float),
+        ("qpos0_block", ctypes.c_int32),
     ]
 
 
@@ -104,12 +108,13 @@ def _u16(a):
 
 def attention(q, k, v, *, G, B, H, M, N, D, scale, strides, mask_mode=MASK_QPOS, qpos=None, qpBs=0,
               bias=None, bias_strides=(0, 0, 0), cu_seqlens=None, key_lo=0, key_hi=0, p_bf16=False,
-              rows=None, precision="f64", nthreads=None):
+              rows=None, precision="f64", nthreads=None, qpos0_block=False):
     """Runs the oracle on flat uint16 (bf16 bits) buffers q, k, v addressed through `strides`:
     strides = dict(qsB, qsH, qsT, qsG, ksB, ksH, ksM, vsB, vsH, vsM), all in elements.
 
     Returns (o, lse) as dense arrays o[B][H][M][D], lse[B][H][M] (float64 or float32). Entries of rows not
-    computed (outside `rows`, or beyond a varlen sequence) are NaN.
+    computed (outside `rows`, or beyond a varlen sequence) are NaN. qpos0_block selects the drop-in entry points'
+    block-wide qpos = 0 rule (reax_fmha_q / reax_fmha_qp); the extension entry points use the per-row rule.
     """
     L = lib()
     q, k, v = _u16(q), _u16(k), _u16(v)
@@ -137,6 +142,7 @@ def attention(q, k, v, *, G, B, H, M, N, D, scale, strides, mask_mode=MASK_QPOS,
     a.key_lo, a.key_hi = key_lo, key_hi
     a.p_bf16 = 1 if p_bf16 else 0
     a.scale = scale
+    a.qpos0_block = 1 if qpos0_block else 0
     dt = np.float64 if precision == "f64" else np.float32
     o = np.full((B, H, M, D), np.nan, dtype=dt)
     lse = np.full((B, H, M), np.nan, dtype=dt)

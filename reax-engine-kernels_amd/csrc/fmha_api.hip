@@ -70,7 +70,8 @@ int reax_fmha_b(const void* q, const void* k, const void* v, const void* bias, v
   return reax::launch_fwd(p, 256, reax::MODE_BIAS, false, static_cast<hipStream_t>(stream));
 }
 
-// qpos mode (reax_fmha_v8.cu:443-450): row r sees keys 0..qpos[b*qpBs + r/G]; row r at r*qsM = (r/G)*(G*qsM) + (r%G)*qsM
+// qpos mode (reax_fmha_v8.cu:443-450): row r sees keys 0..qpos[b*qpBs + r/G]; row r at r*qsM = (r/G)*(G*qsM) + (r%G)*qsM.
+// A 64-row block whose largest qpos is 0 stores V[0] in every row, qpos < 0 rows included (v8:155-162, 224-235).
 int reax_fmha_q(const void* q, const void* k, const void* v, const int* qpos, int G, long long qpBs, void* o,
                 float scale, int B, int H, int M, int N, long long qsB, long long qsH, long long qsM, long long ksB,
                 long long ksH, long long ksM, long long vsB, long long vsH, long long vsM, long long osB, long long osH,
@@ -89,6 +90,7 @@ int reax_fmha_q(const void* q, const void* k, const void* v, const int* qpos, in
   p.osH = osH;
   p.osT = (long long)G * osM;
   p.osG = osM;
+  p.qpos0_block = 1;
   return reax::launch_fwd(p, 256, reax::MODE_QPOS, false, static_cast<hipStream_t>(stream));
 }
 
@@ -115,6 +117,7 @@ int reax_fmha_qp(const void* q, const void* k, const void* v, const int* qpos, i
   p.qg_rs = qg_rs;
   p.outp = static_cast<uint16_t*>(outp);
   p.out_rs = out_rs;
+  p.qpos0_block = 1;
   return reax::launch_fwd(p, 256, reax::MODE_QPOS, true, static_cast<hipStream_t>(stream));
 }
 

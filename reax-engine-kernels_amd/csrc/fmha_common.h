@@ -49,6 +49,11 @@ struct FwdParams {
   int num_splits;
   int split_len;
   int B, H, G, M, N;
+  // The drop-in entry points (reax_fmha_q / reax_fmha_qp) follow the reference's block-wide shortcut: folded rows
+  // of (b, h) form blocks of 64 ([64j, 64j + 64)); when the largest raw qpos of a block's rows is exactly 0, every
+  // row of the block, rows with qpos < 0 included, is stored as V[0] (reax_fmha_v8.cu:155-162, 224-235;
+  // reax_fmha_v11.cu:213-220, 282-293). The extension entry points keep the per-row rule (qpos < 0 -> 0).
+  int qpos0_block;
   int n_tiles;       // row tiles per (b, h)
   float scale;       // softmax scale
   float scale_log2;  // scale * log2(e)

@@ -23,6 +23,7 @@
 #include "fmha_launch.h"
 #include "fmha_tiles.h"
 
+#include <atomic>
 #include <climits>
 #include <type_traits>
 
@@ -37,6 +38,7 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
   __shared__ __align__(1024) uint8_t vbuf0[T::TILE];
   __shared__ __align__(1024) uint8_t vbuf1[T::TILE];
   __shared__ int s_lim[4];
+  __shared__ int s_raw[4];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hf = lane >> 5, lr = lane & 31;
 
   // ---- workgroup -> (batch, KV head, row tile[, key split]): heaviest tile first; when B*H % 8 == 0 each
@@ -75,10 +77,11 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
   const bool rvalid = r < Mb;
   const int tok = rvalid ? r / p.G : 0;
   const int g = rvalid ? r - tok * p.G : 0;
-  int lim = -1;
+  int lim = -1, qraw = -1;
   if (rvalid) {
     if (MODE == MODE_QPOS) {
-      lim = min(p.qpos[(long long)b * p.qpBs + tok], Nb - 1);
+      qraw = p.qpos[(long long)b * p.qpBs + tok];
+      lim = min(qraw, Nb - 1);
     } else if (MODE == MODE_VARLEN) {
       lim = min(tok, Nb - 1);
     } else {
@@ -94,9 +97,23 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
     lim = min(lim, kend - 1);
     if (lim < kbeg) lim = -1;
   }
-  const int wmax = wave_max(lim), wmin = wave_min(lim);
+  const bool blk0 = MODE == MODE_QPOS && !SPLIT && p.qpos0_block;
+  int wmax = wave_max(lim), wmin = wave_min(lim);
+  if (blk0) {
+    // the reference's 64-row blocks start at multiples of 64, so with 128-row tiles wavefronts 2j and 2j + 1 (32
+    // rows each) make up one block: when the block's largest raw qpos is 0, every live row of it sees key 0 only,
+    // which stores V[0] (the raw value: a row with qpos > N - 1 = 0 does not trigger the shortcut)
+    const int rmax = wave_max(qraw);
+    if (lane == 0) s_raw[w] = rmax;
+  }
   if (lane == 0) s_lim[w] = wmax;
   __syncthreads();
+  if (blk0) {
+    const int bmax = max(s_raw[w & ~1], s_raw[w | 1]);
+    if (bmax == 0 && rvalid && Nb > 0) lim = 0;
+    wmax = wave_max(lim);
+    wmin = wave_min(lim);
+  }
   const int cmax = max(max(s_lim[0], s_lim[1]), max(s_lim[2], s_lim[3]));
   const int t_beg = kbeg / T::BN;
   const int t_end = cmax < kbeg ? t_beg : cmax / T::BN + 1;  // key tiles [t_beg, t_end)
@@ -928,17 +945,20 @@ static int prepare(FwdParams& p, bool post) {
   return 0;
 }
 
-// Compute units of the current device (cached per device): the persistent kernels launch one workgroup per CU.
-static int device_cus() {
-  static int cached[64] = {0};
+// Compute units of the device that owns `stream` (the current device for the null stream), cached per device: the
+// persistent kernels launch one workgroup per CU. Entries are atomics, so concurrent first calls from several host
+// threads at worst query the attribute twice and store the same value.
+static int device_cus(hipStream_t stream) {
+  static std::atomic<int> cached[64];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cached[dev] == 0) {
-    int n = 0;
+  if (stream ? hipStreamGetDevice(stream, &dev) != hipSuccess : hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev < 0 || dev >= 64) return 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 template <int MODE>
@@ -946,7 +966,7 @@ static int launch_fwd_pp(FwdParams p, hipStream_t stream) {
   p.n_tiles = (int)(((long long)p.M + PP_BM - 1) / PP_BM);
   const long long n_items = (long long)p.B * p.H * p.n_tiles;
   if (n_items <= 0 || n_items > INT_MAX) return (int)hipErrorInvalidConfiguration;
-  const int cus = device_cus();
+  const int cus = device_cus(stream);
   if (cus <= 0) return (int)hipErrorInvalidDevice;
   const long long nwg = n_items < cus ? n_items : cus;  // one workgroup per CU (its LDS and registers fill one)
   const int o_vec8 = p.o ? (aligned_elems(p.o, 4, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0) : 0;
@@ -958,8 +978,9 @@ int launch_fwd(const FwdParams& p0, int head_dim, int mode, bool post, hipStream
   FwdParams p = p0;
   if (const int rc = prepare(p, post)) return rc;
   // head_dim 128 qpos / varlen without the POST epilogue: the ping-pong kernel once a row tile has enough rows
-  // to fill both groups (short query blocks, e.g. decode, keep the 4-wavefront kernel)
-  if (head_dim == 128 && !post && p.M > FwdTile<128>::BM) {
+  // to fill both groups (short query blocks, e.g. decode, keep the 4-wavefront kernel); the drop-in block rule
+  // (qpos0_block) lives in the 4-wavefront kernel only
+  if (head_dim == 128 && !post && !p.qpos0_block && p.M > FwdTile<128>::BM) {
     if (mode == MODE_QPOS) return launch_fwd_pp<MODE_QPOS>(p, stream);
     if (mode == MODE_VARLEN) return launch_fwd_pp<MODE_VARLEN>(p, stream);
   }

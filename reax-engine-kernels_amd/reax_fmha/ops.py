@@ -58,7 +58,8 @@ def fmha_b(q, k, v, bias, o, scale, *, lib="howu"):
                        bias.stride(0) if bias is not None else 0, bias.stride(1) if bias is not None else 0,
                        bias.stride(2) if bias is not None else 0,
                        o.stride(0), o.stride(1), o.stride(2), _stream())
-    return rc
+    _check("reax_fmha_b", rc)
+    return o
 
 
 def fmha_qp(q, k, v, qpos, G, scale, inv, Lq, qg, out):

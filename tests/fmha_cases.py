@@ -74,8 +74,9 @@ def build(c: Case) -> dict:
     return out
 
 
-def oracle_ref(c: Case, a: dict, *, rows=None, precision="f64", p_bf16=False, key_lo=0, key_hi=0):
-    """(o [B][S][Hq][D], lse [B][Hq][S]) from the CPU oracle; for varlen o [T][Hq][D], lse [T][Hq]."""
+def oracle_ref(c: Case, a: dict, *, rows=None, precision="f64", p_bf16=False, key_lo=0, key_hi=0, dropin=False):
+    """(o [B][S][Hq][D], lse [B][Hq][S]) from the CPU oracle; for varlen o [T][Hq][D], lse [T][Hq]. dropin: the
+    drop-in entry points' block-wide qpos = 0 rule (reax_fmha_q / reax_fmha_qp)."""
     if c.mode == "varlen":
         T = sum(c.seqlens)
         L = max(c.seqlens)
@@ -99,7 +100,7 @@ def oracle_ref(c: Case, a: dict, *, rows=None, precision="f64", p_bf16=False, ke
         kw = dict(mask_mode=pyoracle.MASK_BIAS, bias=a["bias"],
                   bias_strides=(c.Hkv * c.S * c.N, c.S * c.N, c.N))
     else:
-        kw = dict(mask_mode=pyoracle.MASK_QPOS, qpos=a["qpos"], qpBs=c.S)
+        kw = dict(mask_mode=pyoracle.MASK_QPOS, qpos=a["qpos"], qpBs=c.S, qpos0_block=dropin)
     o, lse = pyoracle.attention(a["q"], a["k"], a["v"], G=c.G, B=c.B, H=c.Hkv, M=c.S * c.G, N=c.N, D=c.D,
                                 scale=c.scale, strides=st, rows=rows, precision=precision, p_bf16=p_bf16,
                                 key_lo=key_lo, key_hi=key_hi, **kw)
@@ -143,8 +144,9 @@ def sdpa_ref(c: Case, a: dict):
 def check_tolerance(o_gpu_bits: np.ndarray, o_ref: np.ndarray, lse_gpu=None, lse_ref=None, *,
                     max_abs=2e-2, mean_abs=2e-3, lse_rel=1e-3, where=""):
     """The parity bar: bf16 outputs within max-abs 2e-2 and mean-abs 2e-3 of the double oracle; LSE within
-    1e-3 relative, taken as |dLSE| <= 1e-3 * max(1, |LSE|) (an absolute floor near LSE = 0); -inf LSE must match
-    exactly. Returns a dict of the measured errors."""
+    1e-3 relative: |dLSE| <= 1e-3 * |LSE| + 1e-5 (the 1e-5 absolute term only matters where LSE is within 1e-2 of 0,
+    where a relative bound alone would ask for more than fp32 resolution); -inf LSE must match exactly. Returns a
+    dict of the measured errors (lse_rel = max |dLSE| / (|LSE| + 1e-2))."""
     og = W.bf16_bits_to_f32(o_gpu_bits).astype(np.float64)
     sel = ~np.isnan(o_ref)
     assert np.isfinite(og[sel]).all(), f"{where}: non-finite GPU output"
@@ -157,7 +159,11 @@ def check_tolerance(o_gpu_bits: np.ndarray, o_ref: np.ndarray, lse_gpu=None, lse
         lr, lg = lse_ref[lsel], np.asarray(lse_gpu, dtype=np.float64)[lsel]
         ninf = np.isneginf(lr)
         assert (np.isneginf(lg) == ninf).all(), f"{where}: -inf LSE rows differ"
-        d = np.abs(lg[~ninf] - lr[~ninf]) / np.maximum(1.0, np.abs(lr[~ninf]))
-        res["lse_rel"] = float(d.max()) if d.size else 0.0
-        assert res["lse_rel"] <= lse_rel, f"{where}: LSE rel {res['lse_rel']:.3g} > {lse_rel}"
+        d = np.abs(lg[~ninf] - lr[~ninf])
+        lim = lse_rel * np.abs(lr[~ninf]) + 1e-5
+        res["lse_rel"] = float((d / (np.abs(lr[~ninf]) + 1e-2)).max()) if d.size else 0.0
+        if d.size:
+            worst = int(np.argmax(d - lim))
+            assert (d <= lim).all(), (f"{where}: LSE off by {d[worst]:.3g} at LSE {lr[~ninf][worst]:.6g} "
+                                      f"(bound 1e-3 relative)")
     return res

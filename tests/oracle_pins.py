@@ -220,4 +220,79 @@ def pin_post():
             assert (out[R] == 0x7E00).all(), "rows not named by inv must stay untouched"
 
 
-ALL_PINS = [pin_sdpa, pin_closed_forms, pin_gqa_fold, pin_varlen, pin_split_combine, pin_post, pin_sigmoid]
+def _block_case(name, S, N, Hq, Hkv, qp, seed):
+    return FC.Case(name, B=1, S=S, N=N, Hq=Hq, Hkv=Hkv, D=128, mode="qpos", seed=seed,
+                   qpos=np.asarray(qp, dtype=np.int32).reshape(1, S))
+
+
+def pin_block_rule():
+    """The drop-in entry points' block-wide qpos = 0 rule (reax_fmha_v8.cu:155-162, 224-235), against expectations
+    written out by hand: folded rows r = token*G + g of a KV head form blocks [64j, 64j + 64); a block whose largest
+    raw qpos is 0 stores V[0] in every row (qpos < 0 rows included, LSE = the logit of key 0), any other block
+    follows the per-row rule (qpos < 0 -> 0 / -inf)."""
+    def run(c, dropin):
+        a = FC.build(c)
+        o, lse = FC.oracle_ref(c, a, dropin=dropin)
+        qf = W.bf16_bits_to_f32(a["q"]).astype(np.float64)
+        kf = W.bf16_bits_to_f32(a["k"]).astype(np.float64)
+        vf = W.bf16_bits_to_f32(a["v"]).astype(np.float64)
+        return a, o, lse, qf, kf, vf
+
+    def is_v0(o, lse, qf, kf, vf, c, m, hq, what):
+        h = hq // c.G
+        assert (o[0, m, hq] == vf[0, 0, h]).all(), f"{what}: token {m} head {hq} must store V[0]"
+        _close(lse[0, hq, m], c.scale * float(qf[0, m, hq] @ kf[0, 0, h]), 1e-9, f"{what}: LSE of key 0")
+
+    def is_dead(o, lse, m, hq, what):
+        assert (o[0, m, hq] == 0).all() and np.isneginf(lse[0, hq, m]), f"{what}: token {m} head {hq} must be 0"
+
+    # (1) G = 8: 8 tokens per block. Block 0 = tokens 0..7 with qpos {0, -1 x 7}: every row is V[0] under the
+    # drop-in rule, only token 0 under the per-row rule. Block 1 = tokens 8..15, all -1: nothing visible.
+    qp = [0] + [-1] * 7 + [-1] * 8
+    c = _block_case("block_g8", 16, 20, 8, 1, qp, 91)
+    for dropin in (True, False):
+        a, o, lse, qf, kf, vf = run(c, dropin)
+        for m in range(16):
+            for hq in range(8):
+                if m == 0 or (dropin and m < 8):
+                    is_v0(o, lse, qf, kf, vf, c, m, hq, f"g8 dropin={dropin}")
+                else:
+                    is_dead(o, lse, m, hq, f"g8 dropin={dropin}")
+    # (2) a block whose largest qpos is 3: the per-row rule, also for the drop-in entry points
+    qp = [0, -1, 3, -1, -1, -1, -1, -1]
+    c = _block_case("block_max3", 8, 20, 8, 1, qp, 92)
+    a, o, lse, qf, kf, vf = run(c, True)
+    for hq in range(8):
+        is_v0(o, lse, qf, kf, vf, c, 0, hq, "max3")
+        for m in (1, 3, 4, 5, 6, 7):
+            is_dead(o, lse, m, hq, "max3")
+        assert np.abs(o[0, 2, hq]).sum() > 0 and np.isfinite(lse[0, hq, 2])
+    # (3) G = 3: 64 is not a multiple of G, so token 21's rows 63 (g 0), 64 and 65 (g 1, 2) sit in two blocks.
+    # Block 0 (rows 0..63) has largest qpos 0 (token 5), block 1 (rows 64..89) has 2 (token 25): token 21 g 0 is
+    # V[0], token 21 g 1 and 2 are 0.
+    qp = [-1] * 30
+    qp[5], qp[25] = 0, 2
+    c = _block_case("block_g3", 30, 20, 3, 1, qp, 93)
+    a, o, lse, qf, kf, vf = run(c, True)
+    for m in range(30):
+        for g in range(3):
+            r = 3 * m + g
+            if r < 64:
+                is_v0(o, lse, qf, kf, vf, c, m, g, "g3 block 0")
+            elif m == 25:
+                assert np.isfinite(lse[0, g, m])
+            else:
+                is_dead(o, lse, m, g, "g3 block 1")
+    # (4) N = 1 and a row with qpos 5: the block's raw largest qpos is 5, not 0 (although every visible key
+    # index is clamped to 0), so rows with qpos < 0 stay dead
+    qp = [5, -1, -1, -1, -1, -1, -1, -1]
+    c = _block_case("block_n1", 8, 1, 8, 1, qp, 94)
+    a, o, lse, qf, kf, vf = run(c, True)
+    for hq in range(8):
+        is_v0(o, lse, qf, kf, vf, c, 0, hq, "n1")
+        for m in range(1, 8):
+            is_dead(o, lse, m, hq, "n1")
+
+
+ALL_PINS = [pin_sdpa, pin_closed_forms, pin_gqa_fold, pin_varlen, pin_split_combine, pin_post, pin_sigmoid,
+            pin_block_rule]

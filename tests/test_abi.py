@@ -1,6 +1,6 @@
 """CPU: the drop-in boundary. The two libraries load, export exactly the functions their headers declare (the
 reference's names plus the declared extensions), set no soname, and return the documented codes for calls that
-touch no GPU (NULL bias, not-implemented GDN entry points, workspace sizing)."""
+touch no GPU (NULL bias, the argument guards of the GDN / norm / conv entry points, workspace sizing)."""
 import ctypes
 import os
 import re

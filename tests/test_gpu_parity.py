@@ -1,6 +1,6 @@
 """GPU parity: the HIP kernels, called through the C ABI, against the double-precision CPU oracle (and the
 golden fixtures), to the tolerance of the path: bf16 outputs max-abs <= 2e-2 and mean-abs <= 2e-3, LSE within
-1e-3 relative (|dLSE| <= 1e-3 * max(1, |LSE|)). Large configurations are checked on a seeded subset of tokens
+1e-3 relative (|dLSE| <= 1e-3 * |LSE| + 1e-5). Large configurations are checked on a seeded subset of tokens
 (first and last tokens plus random ones; rows are independent) with every head."""
 import glob
 import os
@@ -171,6 +171,81 @@ def test_reax_fmha_q_dropin(lib, S, G, Hkv):
     FC.check_tolerance(og, oref, where=c.name)
 
 
+def _block_rule_cases():
+    """qpos patterns for the drop-in block-wide qpos = 0 rule (64 folded rows per block, reax_fmha_v8.cu:155-162,
+    224-235): G = 8 blocks {0, -1 x 7}, {-1 x 8}, {0, 0, -1, ...}, {5, -1, 0, ...} (per-row), {-1 ..., 0}; G = 3,
+    where token 21's rows straddle two blocks."""
+    qp8 = np.array([0] + [-1] * 7 + [-1] * 8 + [0, 0] + [-1] * 6 + [5, -1, 0] + [-1] * 5 + [-1] * 7 + [0],
+                   dtype=np.int32)
+    qp3 = np.full(30, -1, dtype=np.int32)
+    qp3[5], qp3[25] = 0, 2
+    return [FC.Case("blk_g8", B=1, S=40, N=50, Hq=16, Hkv=2, D=256, mode="qpos", seed=35, qpos=qp8[None]),
+            FC.Case("blk_g3", B=1, S=30, N=20, Hq=3, Hkv=1, D=256, mode="qpos", seed=36, qpos=qp3[None])]
+
+
+def _v0_rows(c, a):
+    """(token, query head) pairs that the drop-in rule stores as V[0]: rows of blocks whose largest qpos is 0."""
+    out = []
+    qp = a["qpos"][0]
+    M = c.S * c.G
+    for j in range(0, M, 64):
+        rows = range(j, min(j + 64, M))
+        if max(int(qp[r // c.G]) for r in rows) == 0:
+            for h in range(c.Hkv):
+                out += [(r // c.G, h * c.G + r % c.G) for r in rows]
+    return out
+
+
+@pytest.mark.parametrize("lib", ["howu", "post"])
+@pytest.mark.parametrize("ci", [0, 1], ids=["g8", "g3"])
+def test_reax_fmha_q_qpos0_block(lib, ci):
+    """reax_fmha_q applies the reference's block-wide qpos = 0 shortcut: GPU = oracle (drop-in mode) = V[0]
+    bit for bit on every row of a block whose largest qpos is 0, qpos < 0 rows included."""
+    from reax_fmha import ops
+
+    c = _block_rule_cases()[ci]
+    _say(f"reax_fmha_q qpos0 block {lib} {c.name}")
+    a = FC.build(c)
+    G = c.G
+    q = dev(fold(a["q"], G))
+    k, v = dev(a["k"]), dev(a["v"])
+    qpos = torch.from_numpy(a["qpos"]).cuda()
+    o = torch.full_like(q, float("nan"))
+    ops.fmha_q(q, k, v, qpos, G, o, c.scale, lib=lib)
+    torch.cuda.synchronize()
+    og = unfold(host(o), G)
+    oref, _ = FC.oracle_ref(c, a, dropin=True)
+    FC.check_tolerance(og, oref, where=c.name)
+    v0 = _v0_rows(c, a)
+    assert v0, "the case must contain a block whose largest qpos is 0"
+    for m, hq in v0:
+        assert (og[0, m, hq] == a["v"][0, 0, hq // G]).all(), f"token {m} head {hq}: V[0] expected"
+        assert (oref[0, m, hq] == W.bf16_bits_to_f32(a["v"][0, 0, hq // G])).all()
+    dead = [(m, hq) for m in range(c.S) for hq in range(c.Hq) if a["qpos"][0, m] < 0 and (m, hq) not in set(v0)]
+    for m, hq in dead:
+        assert (og[0, m, hq] == 0).all(), f"token {m} head {hq}: 0 expected"
+
+
+def test_reax_fmha_qp_qpos0_block():
+    """The POST path of the block rule: rows of a block whose largest qpos is 0 gate V[0]."""
+    c = _block_rule_cases()[0]
+    _say("reax_fmha_qp qpos0 block")
+    a = FC.build(c)
+    rng = np.random.default_rng(37)
+    T = c.S
+    inv = np.arange(T, dtype=np.int32)
+    qg = W.bf16_normal(rng, (T, c.Hq, 2 * c.D))
+    got = run_post(c, a, qg, inv, T)
+    o, _ = FC.oracle_ref(c, a, dropin=True)
+    want = np.full((T, c.Hq * c.D), 0x7E00, dtype=np.uint16)
+    pyoracle.post_gate(fold_dense(o, c.G), B=1, H=c.Hkv, G=c.G, M=c.S * c.G, D=c.D, inv=inv, Lq=c.S, qg=qg,
+                       qg_rs=c.Hq * 2 * c.D, out=want, out_rs=c.Hq * c.D)
+    for m, hq in _v0_rows(c, a):
+        sl = slice(hq * c.D, (hq + 1) * c.D)
+        assert (got[m, sl] == want[m, sl]).all(), f"token {m} head {hq}: gated V[0] expected bit for bit"
+    FC.check_tolerance(got, W.bf16_bits_to_f32(want).astype(np.float64), where="qp block rule")
+
+
 def run_bias(c, a, lib="howu"):
     from reax_fmha import ops
 
@@ -178,8 +253,7 @@ def run_bias(c, a, lib="howu"):
     k, v = dev(a["k"]), dev(a["v"])
     bias = dev(a["bias"])
     o = torch.full_like(q, float("nan"))
-    rc = ops.fmha_b(q, k, v, bias, o, c.scale, lib=lib)
-    assert rc == 0
+    ops.fmha_b(q, k, v, bias, o, c.scale, lib=lib)
     torch.cuda.synchronize()
     return unfold(host(o), 1)
 

@@ -2,7 +2,8 @@
 
 This shows the pins constrain the oracle: a dropped scale, a wrong GQA head mapping, an off-by-one causal
 boundary, a missing normalisation, a wrong LSE base, a sign error in the sigmoid, the wrong half of the gate
-tensor and an unweighted split combine are each caught.
+tensor, an unweighted split combine, and the drop-in qpos = 0 block rule over tokens instead of rows, on clamped
+instead of raw qpos, or left out are each caught.
 """
 import pytest
 
@@ -10,7 +11,7 @@ import oracle_pins as OP
 import pyoracle
 
 FAST_PINS = [OP.pin_sdpa, OP.pin_closed_forms, OP.pin_gqa_fold, OP.pin_varlen, OP.pin_split_combine, OP.pin_post,
-             lambda: OP.pin_sigmoid(step=97)]
+             lambda: OP.pin_sigmoid(step=97), OP.pin_block_rule]
 
 
 @pytest.mark.parametrize("mutant", sorted(pyoracle.MUTANTS))
