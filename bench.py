@@ -5,7 +5,13 @@ through reax_fmha_qx with LSE output, in causal-adjusted TFLOP/s (FLOPs = 4*Hq*D
 pairs). A "step" is one attention forward over the resident inputs. Also reported in the same line:
   - "roofline": the forward kernel's average duration from HIP events on its stream, against 2516.6 TFLOP/s
     dense bf16 MFMA; "traffic" from the committed rocprofv3 PMC summary when present;
+  - "c1", "c3", "c5": BASELINE configs 1 (causal GQA S 512, reax_fmha_qx), 3 (packed varlen, reax_fmha_varlen)
+    and 5 (S 32768, D 256, sigmoid-gated, through the drop-in reax_fmha_qp of libreax_fmha_post.so), each in
+    TFLOP/s (median over HIP-event-timed launches) with its roofline against the bf16 MFMA peak;
   - "decode": config 4 (split-KV decode + LSE combine) in HBM GB/s against 8 TB/s, L2/MALL flushed between runs;
+  - each config object carries its own "cpu_baseline": the OpenMP fp32 build of the CPU reference (oracle/) on the
+    same inputs (config 5: a seeded sample of query tokens, scaled by its admitted-pair FLOPs), median of 3 runs;
+    the top-level "cpu_baseline" is config 2's;
   - "rarn": the reduce-add RMSNorm (reax_rarn) over 8192 rows of 2560 with 4 partials, HBM GB/s against 8 TB/s;
   - "conv": the causal conv + SiLU + L2 norm (reax_conv_l2, rep 2) over 4096 tokens, HBM GB/s against 8 TB/s;
   - "kkt": the GDN chunk solve (reax_kkt) over 8192 tokens x 16 key heads, GB/s of k read + A written;
@@ -13,8 +19,10 @@ pairs). A "step" is one attention forward over the resident inputs. Also reporte
   - "gemm": the GEMM libraries at a Qwen3-MLP shape (4096 tokens, hidden 2560, intermediate 9728): reax_gv (gate/up
     with the fused SiLU-times-up), reax_gemm (down projection) and reax_slices (the down projection as 4 fp32
     split-K partials), each at its fastest config index, in TFLOP/s against the bf16 MFMA peak, beside torch.matmul
-    (hipBLASLt) on the same operands for reference;
-  - "cpu_baseline": the OpenMP fp32 build of the CPU reference on a bounded sample of config 2's rows.
+    (hipBLASLt) on the same operands for reference.
+The GPU legs run back to back with the headline last (its inputs are resident before the first leg starts), then
+the CPU legs. --trace-summary CSV prints per-(kernel, grid) duration statistics of a rocprofv3 kernel trace, so a
+profile of this command can be split by configuration (configs 1 and 2 run the same kernel).
 Only N = 1 GPU is supported: the path is single-GPU by design.
 """
 import argparse
@@ -38,8 +46,47 @@ def flush_buffer(torch):
     return torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device="cuda")
 
 
-def bench_prefill(torch, ops, steps, warmup):
-    cfg = W.CONFIGS[2]
+def pmc_traffic(path):
+    """HBM bytes per launch of a kernel from a committed rocprofv3 PMC summary, if present."""
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path).read())
+    return float(m.group(1)) if m else None
+
+
+def time_launches(torch, run, warm, iters):
+    """Per-launch durations (ms) from HIP events recorded around each call on torch's current stream, the stream
+    the wrappers pass to the C ABI; `warm` untimed calls first."""
+    for _ in range(warm):
+        run()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    for a, b in evs:
+        a.record()
+        run()
+        b.record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in evs]
+
+
+def mfma_entry(cfg, ms, entry, traffic_path=None, extra=None):
+    """A config's bench object: TFLOP/s of its admitted-pair FLOPs at `ms` per launch, with the roofline against
+    the dense bf16 MFMA peak."""
+    tf = cfg.flops() / (ms * 1e-3) / 1e12
+    e = {"workload": cfg.name, "value": round(tf, 2), "unit": "TFLOP/s", "ms": round(ms, 4),
+         "flops": cfg.flops(), "entry_point": entry,
+         "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": W.BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                      "frac": round(tf / W.BF16_PEAK_TFLOPS, 4),
+                      "traffic": pmc_traffic(traffic_path) if traffic_path else None}}
+    if extra:
+        e.update(extra)
+    return e
+
+
+# ----------------------------------------------------------------------------------------- device inputs
+
+
+def prep_qx(torch, ops, cfg):
+    """Config 1 / 2 inputs resident on the GPU and a closure running reax_fmha_qx (O + LSE) on them."""
     q, k, v, qpos = W.make_prefill_inputs(cfg)
     dev = torch.device("cuda:0")
     qd, kd, vd = (W.bits_to_torch(x, dev) for x in (q, k, v))
@@ -47,25 +94,58 @@ def bench_prefill(torch, ops, steps, warmup):
     o = torch.empty_like(qd)
     lse = torch.empty((cfg.B, cfg.Hq, cfg.S), dtype=torch.float32, device=dev)
     scale = float(np.float32(cfg.scale))
-    run = lambda: ops.attention(qd, kd, vd, qp, scale=scale, o=o, lse=lse)
+    return lambda: ops.attention(qd, kd, vd, qp, scale=scale, o=o, lse=lse)
+
+
+def prep_varlen(torch, ops, cfg):
+    """Config 3 inputs (packed [T][H][D], cu_seqlens) and a closure running reax_fmha_varlen (O + LSE)."""
+    q, k, v, cu = W.make_varlen_inputs(cfg)
+    dev = torch.device("cuda:0")
+    qd, kd, vd = (W.bits_to_torch(x, dev) for x in (q, k, v))
+    cud = torch.from_numpy(cu).to(dev)
+    o = torch.empty_like(qd)
+    lse = torch.empty((qd.shape[0], cfg.Hq), dtype=torch.float32, device=dev)
+    scale = float(np.float32(cfg.scale))
+    L = max(cfg.seqlens)
+    return lambda: ops.attention_varlen(qd, kd, vd, cud, L, scale=scale, o=o, lse=lse)
+
+
+def prep_post(torch, ops, cfg):
+    """Config 5 through the drop-in reax_fmha_qp (libreax_fmha_post.so): Q folded [1][Hkv][S*G][256] (row stride
+    256), K/V [1][S][Hkv][256], qg [S][Hq][512] with the gate logits in the second half, out [S][Hq*256],
+    inv = 0..S-1, causal qpos."""
+    q, k, v, qpos = W.make_prefill_inputs(cfg)
+    gate = W.make_gate(cfg)
+    dev = torch.device("cuda:0")
+    B, S, Hq, D, G = cfg.B, cfg.S, cfg.Hq, cfg.D, cfg.G
+    qf = np.ascontiguousarray(q.reshape(B, S, cfg.Hkv, G, D).transpose(0, 2, 1, 3, 4).reshape(B, cfg.Hkv, S * G, D))
+    qd = W.bits_to_torch(qf, dev)
+    del qf
+    kd, vd = W.bits_to_torch(k, dev), W.bits_to_torch(v, dev)
+    qg = torch.empty((B * S, Hq, 2 * D), dtype=torch.bfloat16, device=dev)
+    qg[:, :, :D] = W.bits_to_torch(q.reshape(B * S, Hq, D), dev)
+    qg[:, :, D:] = W.bits_to_torch(gate, dev)
+    del gate
+    out = torch.empty((B * S, Hq * D), dtype=torch.bfloat16, device=dev)
+    inv = torch.arange(B * S, dtype=torch.int32, device=dev).reshape(B, S)
+    qp = torch.from_numpy(qpos).to(dev)
+    scale = float(np.float32(cfg.scale))
+    return lambda: ops.fmha_qp(qd, kd, vd, qp, G, scale, inv, S, qg, out)
+
+
+def bench_prefill(torch, run, steps, warmup):
+    """The headline: `warmup` untimed forwards, then exactly `steps` timed ones synchronised on both sides (wall
+    clock), then `steps` launches timed with HIP events for the kernel's own duration."""
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
-    # timed region: exactly `steps` forwards, synchronised on both sides
     t0 = time.perf_counter()
     for _ in range(steps):
         run()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps
-    # per-launch kernel duration with HIP events on the launch stream (torch's current stream)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for a, b in evs:
-        a.record()
-        run()
-        b.record()
-    torch.cuda.synchronize()
-    kms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
-    return cfg, wall, kms
+    kms = float(np.mean(time_launches(torch, run, 0, steps)))
+    return wall, kms
 
 
 def bench_decode(torch, ops, iters, num_splits=None):
@@ -100,50 +180,123 @@ def bench_decode(torch, ops, iters, num_splits=None):
     return cfg, ms, gbs
 
 
-def pmc_traffic():
-    """HBM bytes per launch of the forward kernel from the committed rocprofv3 PMC summary, if present."""
-    if not os.path.exists(PMC_SUMMARY):
-        return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(PMC_SUMMARY).read())
-    return float(m.group(1)) if m else None
+# ----------------------------------------------------------------------------------------- CPU baseline
 
 
-def cpu_baseline(target_s=10.0):
-    """OpenMP fp32 CPU reference on a sample of config 2's query tokens (all heads, causal key counts),
-    scaled to TFLOP/s with the sample's own admitted-pair FLOPs."""
+def cpu_threads():
+    """Threads of the CPU baseline: every core this process may run on (sched_getaffinity). Where the host caps
+    a job's CPU share through OMP_NUM_THREADS (the GPU box exports it for a one-GPU job), that cap is honoured.
+    Returns (threads, cores visible)."""
+    try:
+        visible = len(os.sched_getaffinity(0))
+    except AttributeError:
+        visible = os.cpu_count() or 1
+    n = visible
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and 0 < int(env) < n:
+        n = int(env)
+    return max(1, n), visible
+
+
+def _median3(fn):
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def _cpu_entry(value, unit, threads, visible, sample, sec):
+    return dict(value=value, unit=unit, cores=threads, kind="port",
+                sample=f"{sample}; median of 3 runs, {sec:.2f} s each; fp32 OpenMP CPU reference (oracle/), "
+                       f"{threads} threads ({visible} cores visible)")
+
+
+def cpu_prefill(cfg, inputs=None, ntok=None, seed=5):
+    """fp32 OpenMP CPU reference on config 1 / 2 / 5's causal attention (all heads); with ntok a seeded sample of
+    query tokens, each keeping its own causal key count, scaled to TFLOP/s by the sample's admitted-pair FLOPs."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle
 
-    cfg = W.CONFIGS[2]
-    q, k, v, qpos = W.make_prefill_inputs(cfg)
-    try:
-        cores = len(os.sched_getaffinity(0))
-    except AttributeError:
-        cores = os.cpu_count() or 1
-    cores = max(1, min(cores, 16))
+    q, k, v, qpos = inputs if inputs is not None else W.make_prefill_inputs(cfg)
+    threads, visible = cpu_threads()
     st = W.natural_strides(cfg.B, cfg.S, cfg.Hq, cfg.N, cfg.Hkv, cfg.D)
-    rng = np.random.default_rng(5)
+    if ntok is None or ntok >= cfg.S:
+        toks = np.arange(cfg.S)
+    else:
+        toks = np.sort(np.random.default_rng(seed).choice(cfg.S, size=ntok, replace=False))
+    qs = np.ascontiguousarray(q[:, toks])
+    qps = np.ascontiguousarray(qpos[:, toks])
+    sst = dict(st, qsB=len(toks) * cfg.Hq * cfg.D)
+    n = len(toks)
+    fn = lambda: pyoracle.attention(qs, k, v, G=cfg.G, B=cfg.B, H=cfg.Hkv, M=n * cfg.G, N=cfg.N, D=cfg.D,
+                                    scale=float(np.float32(cfg.scale)), strides=sst, qpos=qps, qpBs=n,
+                                    precision="f32", nthreads=threads)
+    sec = _median3(fn)
+    flops = 4 * cfg.Hq * cfg.D * int((qps.astype(np.int64) + 1).sum()) * cfg.B
+    what = (f"{cfg.name}: all {cfg.S} query tokens" if n == cfg.S else
+            f"{cfg.name}: {n} of {cfg.S} query tokens (seeded), each with its causal keys")
+    return _cpu_entry(flops / sec / 1e12, "TFLOP/s", threads, visible,
+                      f"{what} x all {cfg.Hq} heads, {flops / 1e9:.2f} GFLOP", sec)
 
-    def run(ntok):
-        toks = np.sort(rng.choice(cfg.S, size=ntok, replace=False))
-        qs = np.ascontiguousarray(q[:, toks])
-        qps = np.ascontiguousarray(qpos[:, toks])
-        sst = dict(st, qsB=ntok * cfg.Hq * cfg.D)
-        t0 = time.perf_counter()
-        pyoracle.attention(qs, k, v, G=cfg.G, B=1, H=cfg.Hkv, M=ntok * cfg.G, N=cfg.N, D=cfg.D,
-                           scale=float(np.float32(cfg.scale)), strides=sst, qpos=qps, qpBs=ntok, precision="f32",
-                           nthreads=cores)
-        dt = time.perf_counter() - t0
-        flops = 4 * cfg.Hq * cfg.D * int((toks + 1).sum())
-        return ntok, dt, flops
 
-    ntok, dt, flops = run(32)
-    if dt < target_s:
-        ntok = int(min(cfg.S, max(32, 32 * target_s / max(dt, 1e-3))))
-        ntok, dt, flops = run(ntok)
-    return dict(value=flops / dt / 1e12, unit="TFLOP/s", cores=cores, kind="port",
-                sample=f"config 2, {ntok} of {cfg.S} query tokens (seeded) x all {cfg.Hq} heads, causal keys; "
-                       f"{flops / 1e9:.1f} GFLOP in {dt:.1f} s, fp32 OpenMP CPU reference")
+def cpu_varlen(cfg):
+    """fp32 OpenMP CPU reference on all of config 3 (8 packed sequences, per-sequence causal)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+
+    q, k, v, cu = W.make_varlen_inputs(cfg)
+    threads, visible = cpu_threads()
+    L = max(cfg.seqlens)
+    st = dict(qsB=0, qsH=cfg.G * cfg.D, qsT=cfg.Hq * cfg.D, qsG=cfg.D, ksB=0, ksH=cfg.D, ksM=cfg.Hkv * cfg.D,
+              vsB=0, vsH=cfg.D, vsM=cfg.Hkv * cfg.D)
+    fn = lambda: pyoracle.attention(q, k, v, G=cfg.G, B=len(cfg.seqlens), H=cfg.Hkv, M=L * cfg.G, N=L, D=cfg.D,
+                                    scale=float(np.float32(cfg.scale)), strides=st,
+                                    mask_mode=pyoracle.MASK_VARLEN_CAUSAL, cu_seqlens=cu, precision="f32",
+                                    nthreads=threads)
+    sec = _median3(fn)
+    return _cpu_entry(cfg.flops() / sec / 1e12, "TFLOP/s", threads, visible,
+                      f"{cfg.name}: all {len(cfg.seqlens)} sequences {cfg.seqlens} x {cfg.Hq} heads, "
+                      f"{cfg.flops() / 1e9:.2f} GFLOP", sec)
+
+
+def cpu_decode(cfg):
+    """fp32 OpenMP CPU reference on all of config 4 (16 sequences x 8192 cached keys, one query token each), in
+    GB/s of the same compulsory bytes as the GPU figure (K + V + Q + O + LSE)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+
+    q, k, v, qpos = W.make_decode_inputs(cfg)
+    threads, visible = cpu_threads()
+    st = W.natural_strides(cfg.B, cfg.S, cfg.Hq, cfg.N, cfg.Hkv, cfg.D)
+    fn = lambda: pyoracle.attention(q, k, v, G=cfg.G, B=cfg.B, H=cfg.Hkv, M=cfg.S * cfg.G, N=cfg.N, D=cfg.D,
+                                    scale=float(np.float32(cfg.scale)), strides=st, qpos=qpos, qpBs=cfg.S,
+                                    precision="f32", nthreads=threads)
+    sec = _median3(fn)
+    return _cpu_entry(cfg.decode_bytes() / sec / 1e9, "GB/s", threads, visible,
+                      f"{cfg.name}: all {cfg.B} sequences x {cfg.N} keys x {cfg.Hq} heads, "
+                      f"{cfg.decode_bytes() / 1e6:.1f} MB", sec)
+
+
+# ----------------------------------------------------------------------------------------- profile summary
+
+
+def trace_summary(path):
+    """Per-(kernel, grid size) launch statistics of a rocprofv3 kernel-trace CSV (durations in ns): the launches
+    of one configuration share a grid size, so configs that run the same kernel separate."""
+    import csv
+
+    groups = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            key = (row["Kernel_Name"], int(row["Grid_Size_X"]), int(row["Grid_Size_Y"]), int(row["Grid_Size_Z"]))
+            groups.setdefault(key, []).append(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
+    print(f"{'kernel':<72} {'grid':>16} {'calls':>6} {'avg_ns':>10} {'median_ns':>10} {'min_ns':>9} {'max_ns':>9}")
+    for (name, gx, gy, gz), d in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        d = np.array(d)
+        print(f"{name[:72]:<72} {f'{gx}x{gy}x{gz}':>16} {len(d):>6} {d.mean():>10.0f} {np.median(d):>10.0f} "
+              f"{d.min():>9} {d.max():>9}")
 
 
 RARN_N, RARN_S = 8192, 4  # reduce-add RMSNorm leg: 8192 rows of D = 2560, 4 bf16 partials
@@ -334,6 +487,10 @@ def bench_gemm(torch, ops, iters=20):
     return out
 
 
+PROFILES = os.path.join(ROOT, "profiles")
+LEGS = ["prefill", "c1", "c3", "c5", "decode", "rarn", "conv", "kkt", "howu", "gemm"]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -342,16 +499,22 @@ def main():
     # the timed steps measure the sustained rate.
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=300)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "rarn", "conv", "kkt", "howu", "gemm"],
-                    help="run one leg only (for profiling)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the config 1, 3 and 5 legs")
+    ap.add_argument("--only", choices=LEGS, help="run one GPU leg only (for profiling)")
     ap.add_argument("--no-gdn", action="store_true", help="skip the rarn, conv, kkt, howu and gemm legs")
     ap.add_argument("--decode-splits", type=int, default=0, help="override config 4's key-split count")
+    ap.add_argument("--iters", type=int, default=20, help="timed launches per config leg (median reported)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="only run a 256 MiB device-to-device copy 5 times: the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="print per-(kernel, grid) statistics of a rocprofv3 kernel-trace CSV and exit")
     args = ap.parse_args()
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
     if args.calib_copy:
         import torch
 
@@ -370,40 +533,103 @@ def main():
 
     from reax_fmha import ops
 
-    if args.only == "gemm":
+    one = args.only
+    if one == "gemm":
         print(json.dumps(bench_gemm(torch, ops)), flush=True)
         return
-    if args.only == "howu":
+    if one == "howu":
         ms, tf = bench_howu(torch, ops)
         print(json.dumps({"howu_TFLOPs": round(tf, 2), "ms": round(ms, 4), "seqs": HOWU_N, "tokens": HOWU_T}),
               flush=True)
         return
-    if args.only == "kkt":
+    if one == "kkt":
         ms, gbs = bench_kkt(torch, ops)
         print(json.dumps({"kkt_GBs": round(gbs, 1), "ms": round(ms, 4), "tokens": KKT_T, "key_heads": KKT_H}),
               flush=True)
         return
-    if args.only == "conv":
+    if one == "conv":
         ms, gbs = bench_conv(torch, ops)
         print(json.dumps({"conv_GBs": round(gbs, 1), "ms": round(ms, 4), "tokens": CONV_T}), flush=True)
         return
-    if args.only == "rarn":
+    if one == "rarn":
         ms, gbs = bench_rarn(torch, ops)
         print(json.dumps({"rarn_GBs": round(gbs, 1), "ms": round(ms, 4), "rows": RARN_N, "partials": RARN_S}),
               flush=True)
         return
-    if args.only == "decode":
+    if one == "decode":
         dcfg, dms, gbs = bench_decode(torch, ops, args.steps, args.decode_splits)
         print(json.dumps({"decode_GBs": round(gbs, 1), "ms": round(dms, 4), "splits": dcfg.num_splits}), flush=True)
         return
-    cfg, wall, kms = bench_prefill(torch, ops, args.steps, args.warmup)
-    if args.only == "prefill":
+
+    # config legs: inputs resident on the GPU before any timing
+    preps = {
+        "c1": (lambda: prep_qx(torch, ops, W.CONFIGS[1]), W.CONFIGS[1], "reax_fmha_qx (libreax_howu.so)"),
+        "c3": (lambda: prep_varlen(torch, ops, W.CONFIGS[3]), W.CONFIGS[3], "reax_fmha_varlen (libreax_howu.so)"),
+        "c5": (lambda: prep_post(torch, ops, W.CONFIGS[5]), W.CONFIGS[5],
+               "reax_fmha_qp (libreax_fmha_post.so): drop-in ABI, sigmoid gate epilogue"),
+    }
+    traffic = {"c1": None, "c3": os.path.join(PROFILES, "fmha_fwd_c3_pmc.txt"),
+               "c5": os.path.join(PROFILES, "fmha_fwd_c5_pmc.txt")}
+    if one in preps:
+        mk, cfg, entry = preps[one]
+        ms = float(np.median(time_launches(torch, mk(), args.warmup, args.iters)))
+        print(json.dumps(mfma_entry(cfg, ms, entry, traffic[one])), flush=True)
+        return
+
+    cfg = W.CONFIGS[2]
+    run2 = prep_qx(torch, ops, cfg)
+    if one == "prefill":
+        wall, kms = bench_prefill(torch, run2, args.steps, args.warmup)
         print(json.dumps({"TFLOPs": round(cfg.flops() / wall / 1e12, 2), "kernel_ms": round(kms, 4)}), flush=True)
         return
+
+    legs = {}
+    if not args.no_decode:
+        dcfg, dms, gbs = bench_decode(torch, ops, 20)
+        legs["decode"] = {"workload": dcfg.name, "value": round(gbs, 1), "unit": "GB/s", "ms": round(dms, 4),
+                          "bytes": dcfg.decode_bytes(), "num_splits": dcfg.num_splits,
+                          "entry_point": "reax_fmha_splitkv (libreax_howu.so): split kernel + LSE combine kernel",
+                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
+                                       "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4),
+                                       "traffic": pmc_traffic(os.path.join(PROFILES, "fmha_decode_c4_pmc.txt"))}}
+    if not args.no_configs:
+        for name in ("c1", "c3", "c5"):
+            mk, ccfg, entry = preps[name]
+            run = mk()
+            ms = float(np.median(time_launches(torch, run, 10, args.iters)))
+            del run
+            legs[name] = mfma_entry(ccfg, ms, entry, traffic[name])
+            torch.cuda.empty_cache()
+    if not args.no_gdn:
+        ms, gbs = bench_rarn(torch, ops)
+        legs["rarn"] = {"workload": f"reax_rarn {RARN_N} rows x 2560, {RARN_S} partials", "value": round(gbs, 1),
+                        "unit": "GB/s", "ms": round(ms, 4),
+                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
+                                     "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
+        ms, gbs = bench_conv(torch, ops)
+        legs["conv"] = {"workload": f"reax_conv_l2 {CONV_T} tokens, KD {CONV_KD}, VD {CONV_VD}, rep 2",
+                        "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
+                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
+                                     "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
+        ms, gbs = bench_kkt(torch, ops)
+        legs["kkt"] = {"workload": f"reax_kkt {KKT_T} tokens, {KKT_H} key heads", "value": round(gbs, 1),
+                       "unit": "GB/s", "ms": round(ms, 4),
+                       "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
+                                    "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
+        ms, tf = bench_howu(torch, ops)
+        legs["howu"] = {"workload": f"reax_howu {HOWU_N} x {HOWU_T} tokens, {HOWU_H} key / {2 * HOWU_H} value heads",
+                        "value": round(tf, 2), "unit": "TFLOP/s", "ms": round(ms, 4),
+                        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": W.BF16_PEAK_TFLOPS,
+                                     "unit": "TFLOP/s", "frac": round(tf / W.BF16_PEAK_TFLOPS, 4)}}
+        g = bench_gemm(torch, ops)
+        legs["gemm"] = {"workload": f"MLP {GEMM_M} tokens, hidden {GEMM_HID}, intermediate {GEMM_INTER}; slices S "
+                                    f"{GEMM_S} fp32", **g}
+
+    # the headline, last among the GPU legs
+    wall, kms = bench_prefill(torch, run2, args.steps, args.warmup)
     flops = cfg.flops()
     value = flops / wall / 1e12
     achieved = flops / (kms * 1e-3) / 1e12
-    traffic = pmc_traffic()
     line = {
         "metric": "causal attention TFLOP/s on 1 MI355X (% of bf16 MFMA peak); decode HBM GB/s",
         "value": round(value, 2),
@@ -421,41 +647,23 @@ def main():
                    "causal": True, "flops_per_step": flops, "entry_point": "reax_fmha_qx (libreax_howu.so)"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": W.BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / W.BF16_PEAK_TFLOPS, 4),
-                     "traffic": traffic, "kernel_ms": round(kms, 4)},
+                     "traffic": pmc_traffic(PMC_SUMMARY), "kernel_ms": round(kms, 4)},
     }
-    if not args.no_decode:
-        dcfg, dms, gbs = bench_decode(torch, ops, 20)
-        line["decode"] = {"workload": dcfg.name, "value": round(gbs, 1), "unit": "GB/s", "ms": round(dms, 4),
-                          "bytes": dcfg.decode_bytes(), "num_splits": dcfg.num_splits,
-                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
-                                       "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
-    if not args.no_gdn:
-        ms, gbs = bench_rarn(torch, ops)
-        line["rarn"] = {"workload": f"reax_rarn {RARN_N} rows x 2560, {RARN_S} partials", "value": round(gbs, 1),
-                        "unit": "GB/s", "ms": round(ms, 4),
-                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
-                                     "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
-        ms, gbs = bench_conv(torch, ops)
-        line["conv"] = {"workload": f"reax_conv_l2 {CONV_T} tokens, KD {CONV_KD}, VD {CONV_VD}, rep 2",
-                        "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
-                        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
-                                     "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
-        ms, gbs = bench_kkt(torch, ops)
-        line["kkt"] = {"workload": f"reax_kkt {KKT_T} tokens, {KKT_H} key heads", "value": round(gbs, 1),
-                       "unit": "GB/s", "ms": round(ms, 4),
-                       "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
-                                    "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4)}}
-        ms, tf = bench_howu(torch, ops)
-        line["howu"] = {"workload": f"reax_howu {HOWU_N} x {HOWU_T} tokens, {HOWU_H} key / {2 * HOWU_H} value heads",
-                        "value": round(tf, 2), "unit": "TFLOP/s", "ms": round(ms, 4),
-                        "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": W.BF16_PEAK_TFLOPS,
-                                     "unit": "TFLOP/s", "frac": round(tf / W.BF16_PEAK_TFLOPS, 4)}}
-        g = bench_gemm(torch, ops)
-        line["gemm"] = {"workload": f"MLP {GEMM_M} tokens, hidden {GEMM_HID}, intermediate {GEMM_INTER}; slices S "
-                                    f"{GEMM_S} fp32", **g}
+    line.update(legs)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline()
+        line["cpu_baseline"] = cpu_prefill(cfg)
+        if "c1" in line:
+            line["c1"]["cpu_baseline"] = cpu_prefill(W.CONFIGS[1])
+        if "c3" in line:
+            line["c3"]["cpu_baseline"] = cpu_varlen(W.CONFIGS[3])
+        if "decode" in line:
+            line["decode"]["cpu_baseline"] = cpu_decode(W.CONFIGS[4])
+        if "c5" in line:
+            line["c5"]["cpu_baseline"] = cpu_prefill(W.CONFIGS[5], ntok=CPU_C5_TOKENS)
     print(json.dumps(line), flush=True)
+
+
+CPU_C5_TOKENS = 96  # config 5's CPU baseline sample: seeded query tokens (x all 16 heads, each its causal keys)
 
 
 if __name__ == "__main__":
