@@ -75,6 +75,20 @@ int reax_fmha_splitkv(const void* q, const void* k, const void* v, const int* qp
                       long long osH, long long osT, long long osG, long long lsB, long long lsH, long long lsT,
                       long long lsG, void* stream);
 
+/* reax_fmha_splitkv without a workspace argument, for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc); it has no counterpart in the reference. The partials go
+ * to a static device array of 8 MiB that each GPU the library runs on holds until the process ends; nothing on the
+ * call path allocates. Same arguments (minus ws / ws_bytes), kernels and result as reax_fmha_splitkv. Returns
+ * hipErrorOutOfMemory (2) when reax_fmha_splitkv_workspace(B, H, M, D, num_splits) exceeds 8 MiB (config 4, B 16,
+ * 8 KV heads, 4 rows, 16 splits, needs 4.2 MB). Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU race (order them on one stream). */
+int reax_fmha_splitkv_noalloc(const void* q, const void* k, const void* v, const int* qpos, int G, long long qpBs,
+                              void* o, float* lse, float scale, int B, int H, int M, int N, int D, int num_splits,
+                              long long qsB, long long qsH, long long qsT, long long qsG, long long ksB,
+                              long long ksH, long long ksM, long long vsB, long long vsH, long long vsM,
+                              long long osB, long long osH, long long osT, long long osG, long long lsB,
+                              long long lsH, long long lsT, long long lsG, void* stream);
+
 /* ---- 3. the reference's Gated-DeltaNet / norm / conv entry points ------------------------------------------ */
 
 /* Reduce-add RMSNorm. Replaces reax_rarn, libreax_howu/reax_rarn_final.cu:98-106. Rows of D = 2560 bf16:

@@ -214,6 +214,37 @@ int reax_fmha_splitkv(const void* q, const void* k, const void* v, const int* qp
   return reax::launch_splitkv(sp, D, static_cast<hipStream_t>(stream));
 }
 
+int reax_fmha_splitkv_noalloc(const void* q, const void* k, const void* v, const int* qpos, int G, long long qpBs,
+                              void* o, float* lse, float scale, int B, int H, int M, int N, int D, int num_splits,
+                              long long qsB, long long qsH, long long qsT, long long qsG, long long ksB,
+                              long long ksH, long long ksM, long long vsB, long long vsH, long long vsM,
+                              long long osB, long long osH, long long osT, long long osG, long long lsB,
+                              long long lsH, long long lsT, long long lsG, void* stream) {
+  if (!qpos) return (int)hipErrorInvalidValue;
+  reax::SplitParams sp{};
+  FwdParams& p = sp.f;
+  p = base_params(q, k, v, o, scale, B, H, M, N);
+  p.qpos = qpos;
+  p.qpBs = qpBs;
+  p.G = G;
+  p.lse = lse;
+  p.qsB = qsB;
+  p.qsH = qsH;
+  p.qsT = qsT;
+  p.qsG = qsG;
+  set_kv(p, ksB, ksH, ksM, vsB, vsH, vsM);
+  p.osB = osB;
+  p.osH = osH;
+  p.osT = osT;
+  p.osG = osG;
+  p.lsB = lsB;
+  p.lsH = lsH;
+  p.lsT = lsT;
+  p.lsG = lsG;
+  sp.num_splits = num_splits;
+  return reax::launch_splitkv_noalloc(sp, D, static_cast<hipStream_t>(stream));
+}
+
 #endif
 
 }  // extern "C"

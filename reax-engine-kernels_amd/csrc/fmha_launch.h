@@ -22,4 +22,10 @@ struct SplitParams {
 size_t splitkv_workspace_bytes(int B, int H, int M, int head_dim, int num_splits);
 int launch_splitkv(const SplitParams& p, int head_dim, hipStream_t stream);
 
+// The same with the library's per-device static scratch as the workspace (p.ws / p.ws_bytes are ignored): no
+// allocation anywhere on the call path. Returns hipErrorOutOfMemory when the workspace the shape needs exceeds
+// SPLITKV_SCRATCH_BYTES (fmha_noalloc.hip).
+constexpr size_t SPLITKV_SCRATCH_BYTES = size_t(8) << 20;
+int launch_splitkv_noalloc(SplitParams p, int head_dim, hipStream_t stream);
+
 }  // namespace reax

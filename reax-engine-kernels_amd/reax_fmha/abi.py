@@ -29,6 +29,7 @@ SIGNATURES = {
     "reax_fmha_varlen": [P, P, P, P, I, I, P, P, F, I, I, I] + [LL] * 10 + [P],
     "reax_fmha_splitkv_workspace": [I, I, I, I, I],
     "reax_fmha_splitkv": [P, P, P, P, I, LL, P, P, F, I, I, I, I, I, I, P, SZ] + [LL] * 18 + [P],
+    "reax_fmha_splitkv_noalloc": [P, P, P, P, I, LL, P, P, F, I, I, I, I, I, I] + [LL] * 18 + [P],
     "howu3_dense": [P, P, P, P, P, P, P, P, F, I, I, I, P],
     "howu3_skip": [P, P, P, P, P, P, P, P, F, I, I, I, P],
     "howu3_smem": [],
@@ -54,7 +55,7 @@ RESTYPES = {"reax_fmha_splitkv_workspace": SZ, "reax_gemm_cfgname": ctypes.c_cha
             "reax_slices_cfgname": ctypes.c_char_p, "reax_gv_cfgname": ctypes.c_char_p}
 
 HOWU_SYMBOLS = ["reax_fmha_b", "reax_fmha_q", "reax_fmha_qx", "reax_fmha_varlen", "reax_fmha_splitkv_workspace",
-                "reax_fmha_splitkv", "howu3_dense", "howu3_skip", "howu3_smem", "reax_howu", "reax_kkt",
+                "reax_fmha_splitkv", "reax_fmha_splitkv_noalloc", "howu3_dense", "howu3_skip", "howu3_smem", "reax_howu", "reax_kkt",
                 "reax_kkt_smem", "reax_rarn", "reax_howu_norm", "reax_conv_l2", "reax_conv_v"]
 POST_SYMBOLS = ["reax_fmha_b", "reax_fmha_q", "reax_fmha_qp"]
 PLAIN_SYMBOLS = ["reax_gemm_ncfg", "reax_gemm_cfgname", "reax_gemm"]

@@ -151,6 +151,25 @@ def attention_splitkv(q, k, v, qpos, *, scale, num_splits, ws=None, o=None, lse=
     return o, lse
 
 
+def attention_splitkv_noalloc(q, k, v, qpos, *, scale, num_splits, o, lse=None):
+    """reax_fmha_splitkv_noalloc on natural layouts (as attention_splitkv): the library's static per-GPU scratch
+    is the workspace, so the call allocates nothing; o (and lse, if wanted) must be given."""
+    _dev(q, k, v, qpos, o, lse)
+    B, S, Hq, D = q.shape
+    N, Hkv = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    ls = lse.stride() if lse is not None else (0, 0, 0)
+    rc = abi.howu().reax_fmha_splitkv_noalloc(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), qpos.data_ptr(), G, qpos.stride(0), o.data_ptr(), _ptr(lse),
+        scale, B, Hkv, S * G, N, D, num_splits,
+        q.stride(0), G * q.stride(2), q.stride(1), q.stride(2),
+        k.stride(0), k.stride(2), k.stride(1), v.stride(0), v.stride(2), v.stride(1),
+        o.stride(0), G * o.stride(2), o.stride(1), o.stride(2),
+        ls[0], G * ls[1], ls[2], ls[1], _stream())
+    _check("reax_fmha_splitkv_noalloc", rc)
+    return o, lse
+
+
 def rarn(part, S, serial, pstride, res, w, n, *, eps, factor, h_out=None, out=None, D=2560):
     """reax_rarn (libreax_howu/reax_rarn_final.cu:98-106) on device tensors: part is a bf16 buffer holding S
     partials of (n, D) rows, pstride elements apart; res (n, D), w (D,). Returns (h_out, out), each (n, D) bf16."""

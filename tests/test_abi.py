@@ -140,6 +140,17 @@ def test_gemm_argument_codes():
     assert G.reax_gv(0, None, None, None, 8, 2 ** 30 + 4, 8, None) == 3     # 2 N2 beyond int
 
 
+def test_splitkv_noalloc_rejects_oversize():
+    # partials of B 64 x 8 KV heads x 64 splits x 4 rows x 129 floats (67.6 MB) exceed the 8 MiB static scratch:
+    # hipErrorOutOfMemory before any HIP call; a NULL qpos is hipErrorInvalidValue as for reax_fmha_splitkv
+    L = abi.howu()
+    dummy = ctypes.c_int(0)
+    args = [None, None, None, ctypes.addressof(dummy), 4, 1, None, None, 0.088, 64, 8, 4, 8192, 128, 64] + [0] * 18
+    assert L.reax_fmha_splitkv_noalloc(*args, None) == 2
+    args[3] = None
+    assert L.reax_fmha_splitkv_noalloc(*args, None) == 1
+
+
 def test_splitkv_workspace_size():
     L = abi.howu()
     # config 4: B 16, Hkv 8, M = G = 4 rows, D 128, 16 splits: partial O fp32 + LSE fp32, each 256-byte aligned
