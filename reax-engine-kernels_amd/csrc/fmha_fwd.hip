@@ -911,12 +911,6 @@ __global__ void __launch_bounds__(256) splitkv_combine_kernel(const FwdParams p)
 
 // ------------------------------------------------------------------------------------------------ host side
 
-static bool aligned_elems(const void* ptr, long long n_elems_multiple, std::initializer_list<long long> strides) {
-  if ((reinterpret_cast<uintptr_t>(ptr) & (uintptr_t)(2 * n_elems_multiple - 1)) != 0) return false;
-  for (long long s : strides)
-    if (s % n_elems_multiple != 0) return false;
-  return true;
-}
 
 template <int HD, int MODE, bool POST, bool SPLIT>
 static int launch_fwd_t(const FwdParams& p, hipStream_t stream) {
@@ -948,7 +942,7 @@ static int prepare(FwdParams& p, bool post) {
 // Compute units of the device that owns `stream` (the current device for the null stream), cached per device: the
 // persistent kernels launch one workgroup per CU. Entries are atomics, so concurrent first calls from several host
 // threads at worst query the attribute twice and store the same value.
-static int device_cus(hipStream_t stream) {
+int device_cus(hipStream_t stream) {
   static std::atomic<int> cached[64];
   int dev = 0;
   if (stream ? hipStreamGetDevice(stream, &dev) != hipSuccess : hipGetDevice(&dev) != hipSuccess) return 0;
@@ -984,6 +978,10 @@ int launch_fwd(const FwdParams& p0, int head_dim, int mode, bool post, hipStream
     if (mode == MODE_QPOS) return launch_fwd_pp<MODE_QPOS>(p, stream);
     if (mode == MODE_VARLEN) return launch_fwd_pp<MODE_VARLEN>(p, stream);
   }
+  // head_dim 256 qpos / varlen (the drop-in shape, with or without the POST epilogue): the wavefront-pair
+  // ping-pong kernel once there are rows for both of its groups (fmha_fwd_pair.hip)
+  if (head_dim == 256 && (mode == MODE_QPOS || (mode == MODE_VARLEN && !post)) && p.M > 64)
+    return launch_fwd_pair(p, mode, post, stream);
   if (head_dim == 128) {
     if (mode == MODE_QPOS)
       return post ? launch_fwd_t<128, MODE_QPOS, true, false>(p, stream) : launch_fwd_t<128, MODE_QPOS, false, false>(p, stream);
