@@ -15,12 +15,14 @@
 // (the dispatcher deals a workgroup's wavefronts round-robin over the CU's 4 SIMDs), and the groups ping-pong as in
 // the head_dim-128 kernel:
 //     half 1 of step t: group 0 runs its MFMA phase  [S(t) = Q K(t)^T, then O += P(t-1) V(t-1)]
-//                       group 1 runs its VALU phase  [softmax of S(t-1), then the K(t+1) / V(t) tile loads]
-//     half 2 of step t: group 1 runs its MFMA phase, group 0 the softmax of S(t).
+//                       group 1 runs its VALU phase  [softmax of S(t-1), then the K(t+1) tile loads]
+//     half 2 of step t: group 1 runs its MFMA phase, group 0 the V(t) tile loads and the softmax of S(t).
 // The row maxima of S(t) are computed at the end of the MFMA phase (while the P.V MFMAs run) and published at the
 // next barrier; the probabilities at the end of the softmax phase, for the partner's next MFMA phase. The softmax
-// phase is about half as long as an MFMA phase, so group 1 issues all of a step's direct-to-LDS tile loads from
-// inside its softmax phase, where they cost no matrix-core time.
+// phase is about half as long as an MFMA phase, so the direct-to-LDS tile loads (64 KB per step) are issued from
+// the softmax phases, where they cost no matrix-core time: K(t+1) by group 1 in half 1, V(t) by group 0 in half 2.
+// (Issued all in half 1, with group 1's softmax, they made that half longer than the MFMA phase opposite it:
+// config 5 ran 9.9 ms that way and 8.65 ms split.)
 #include "fmha_common.h"
 #include "fmha_launch.h"
 #include "fmha_tiles.h"
@@ -279,9 +281,13 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pair_kernel(const FwdParams p
         }
       }
     };
-    // group 1's loads of step t: K(t+1) and V(t)
-    auto loads = [&](int t) __attribute__((always_inline)) {
+    // the loads of step t, split over both halves so that the memory pipeline streams through the whole step:
+    // K(t+1) by group 1 in half 1 (after its softmax), V(t) by group 0 at the start of half 2 (before its
+    // softmax); both land before the end-of-step barrier
+    auto load_k = [&](int t) __attribute__((always_inline)) {
       if (t + 1 < t_end) tile_load(kring[(t + 1) & 1], Kb, p.ksM, kfast, (t + 1) * T::BN);
+    };
+    auto load_v = [&](int t) __attribute__((always_inline)) {
       if (t < t_end) tile_load(vring[t & 1], Vb, p.vsM, vfast, t * T::BN);
     };
 
@@ -296,17 +302,18 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pair_kernel(const FwdParams p
           mfma_phase(t, kb_t, vb_prev);
         } else {
           if (t >= 1) softmax(t - 1);
-          loads(t);
+          load_k(t);
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's xm / xp writes are visible ...
         exec_barrier();                      // ... to its partner after the barrier (the tile loads stay in flight)
         if (grp == 0) {
+          load_v(t);
           if (t < t_end) softmax(t);
         } else {
           mfma_phase(t, kb_t, vb_prev);
         }
-        // K(t+1) and V(t), issued by group 1 in this step, must have landed (vmcnt(0)); every wavefront is done
-        // with K(t) and V(t-1), which the next step's loads replace
+        // K(t+1) and V(t), issued in this step, must have landed (vmcnt(0)); every wavefront is done with K(t)
+        // and V(t-1), which the next step's loads replace
         __builtin_amdgcn_s_waitcnt(0x0F70);
         __syncthreads();
       }
