@@ -21,6 +21,7 @@
 //     first (v8:134-135) and, when B*H is a multiple of 8, each XCD's L2 serves a fixed set of KV heads.
 #include "fmha_common.h"
 #include "fmha_launch.h"
+#include "fmha_sched.h"
 #include "fmha_tiles.h"
 
 #include <atomic>
@@ -349,6 +350,7 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   __shared__ __align__(1024) uint8_t kring[NS][T::TILE];
   __shared__ __align__(1024) uint8_t vring[NS][T::TILE];
   __shared__ int s_lim[PP_NW];
+  __shared__ std::conditional_t<MODE == MODE_VARLEN, VarlenSched, char> vs;  // varlen item schedule
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hf = lane >> 5, lr = lane & 31;
   const int grp = w >> 2;
   const uint32_t wu = __builtin_amdgcn_readfirstlane(w);  // the wavefront index as a scalar, for load addresses
@@ -363,17 +365,8 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   const int BH = p.B * p.H;
   const long long n_items = (long long)BH * p.n_tiles;
   const bool xcd_aware = MODE != MODE_VARLEN && (BH & 7) == 0 && (gridDim.x & 7) == 0;
-  auto item = [&](int id) __attribute__((always_inline)) {
-  int bh, rank;
-  if (xcd_aware) {
-    const int per = BH >> 3, x = id & 7, j = id >> 3;
-    bh = x + 8 * (j % per);
-    rank = j / per;
-  } else {
-    bh = id % BH;
-    rank = id / BH;
-  }
-  const int tile = p.n_tiles - 1 - rank;
+  // item (bh, tile): row tile `tile` of (batch or sequence bh / H, KV head bh % H)
+  auto item = [&](int bh, int tile) __attribute__((always_inline)) {
   const int b = bh / p.H, hk = bh - b * p.H;
   long long tok0 = 0;
   int Mb = p.M, Nb = p.N;
@@ -648,6 +641,21 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   };  // item
 
   const int P = gridDim.x;
+  if constexpr (MODE == MODE_VARLEN) {
+    // packed sequences: the batched longest-first schedule of fmha_sched.h, computed alike by every workgroup
+    vs_build<PP_BM>(vs, p.cu_seqlens, p.B, p.H, p.G, P, (int)blockIdx.x);
+    if (vs.ok) {
+      for (int r = 0; r < vs.rounds; ++r) {
+        const int k = vs.mine[r];
+        if (k < 0) continue;
+        int rank, head, level;
+        vs_decode(vs, p.H, (int)blockIdx.x % vs.nx, k, rank, head, level);
+        exec_barrier();  // as below
+        item(vs.sorted[rank] * p.H + head, level);
+      }
+      return;
+    }
+  }
   for (int it = 0;; ++it) {
     long long vid;
     if (xcd_aware) {
@@ -657,11 +665,21 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
       vid = (long long)it * P + ((it & 1) ? P - 1 - (int)blockIdx.x : (int)blockIdx.x);
     }
     if (vid >= n_items) break;
+    const int id = (int)vid;
+    int bh, rank;
+    if (xcd_aware) {
+      const int per = BH >> 3, x = id & 7, j = id >> 3;
+      bh = x + 8 * (j % per);
+      rank = j / per;
+    } else {
+      bh = id % BH;
+      rank = id / BH;
+    }
     // every wavefront is done with the previous item's s_lim and K/V buffers (its last LDS read was followed by a
     // full barrier). Not __syncthreads(): its fence would wait for the previous item's output stores, whose
     // latency instead overlaps the next item's first loads.
     exec_barrier();
-    item((int)vid);
+    item(bh, p.n_tiles - 1 - rank);
   }
 }
 
