@@ -388,7 +388,9 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
     lim = MODE == MODE_QPOS ? min(p.qpos[(long long)b * p.qpBs + tok], Nb - 1) : min(tok, Nb - 1);
     lim = max(lim, -1);
   }
-  const int wmax = wave_max(lim), wmin = wave_min(lim);
+  // wmin: the smallest limit among the wavefront's rows inside the tile. Rows past its end are never stored, so
+  // they must not force the mask pass onto every key tile of a partial row tile.
+  const int wmax = wave_max(lim), wmin = wave_min(rvalid ? lim : INT_MAX);
   if (lane == 0) s_lim[w] = wmax;
   __syncthreads();
   int cmax = s_lim[0];
