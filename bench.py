@@ -21,7 +21,9 @@ pairs). A "step" is one attention forward over the resident inputs. Also reporte
     split-K partials), each at its fastest config index, in TFLOP/s against the bf16 MFMA peak, beside torch.matmul
     (hipBLASLt) on the same operands for reference.
 The GPU legs run back to back with the headline last (its inputs are resident before the first leg starts), then
-the CPU legs. --trace-summary CSV prints per-(kernel, grid) duration statistics of a rocprofv3 kernel trace, so a
+the CPU legs. --pmc-clock CSV prints the shader clock per kernel from a GRBM_GUI_ACTIVE counter run (with --only
+prefill --const-inputs: the same forward on constant inputs, for the clock's dependence on the data).
+--trace-summary CSV prints per-(kernel, grid) duration statistics of a rocprofv3 kernel trace, so a
 profile of this command can be split by configuration (configs 1 and 2 run the same kernel).
 Only N = 1 GPU is supported: the path is single-GPU by design.
 """
@@ -85,11 +87,15 @@ def mfma_entry(cfg, ms, entry, traffic_path=None, extra=None):
 # ----------------------------------------------------------------------------------------- device inputs
 
 
-def prep_qx(torch, ops, cfg):
-    """Config 1 / 2 inputs resident on the GPU and a closure running reax_fmha_qx (O + LSE) on them."""
+def prep_qx(torch, ops, cfg, const_inputs=False):
+    """Config 1 / 2 inputs resident on the GPU and a closure running reax_fmha_qx (O + LSE) on them. const_inputs:
+    q, k, v all 2^-7 (the same work and memory traffic on inputs that toggle few bits: the clock measurement)."""
     q, k, v, qpos = W.make_prefill_inputs(cfg)
     dev = torch.device("cuda:0")
     qd, kd, vd = (W.bits_to_torch(x, dev) for x in (q, k, v))
+    if const_inputs:
+        for x in (qd, kd, vd):
+            x.fill_(2.0 ** -7)
     qp = torch.from_numpy(qpos).to(dev)
     o = torch.empty_like(qd)
     lse = torch.empty((cfg.B, cfg.Hq, cfg.S), dtype=torch.float32, device=dev)
@@ -280,6 +286,29 @@ def cpu_decode(cfg):
 
 
 # ----------------------------------------------------------------------------------------- profile summary
+
+
+def pmc_clock(path):
+    """Shader clock per kernel from a rocprofv3 --pmc GRBM_GUI_ACTIVE counter CSV: the counter (GPU-busy cycles,
+    reported per dispatch summed over the MI355X's 8 XCDs) divided by 8 and by the dispatch's duration; mean over
+    the last half of each kernel's dispatches (past the clock ramp). Meaningful for long dispatches only."""
+    import csv
+
+    disp = {}
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] != "GRBM_GUI_ACTIVE":
+                continue
+            key = (row["Kernel_Name"], int(row["Dispatch_Id"]))
+            d = disp.setdefault(key, [0.0, int(row["End_Timestamp"]) - int(row["Start_Timestamp"])])
+            d[0] += float(row["Counter_Value"])
+    per = {}
+    for (name, did), (cyc, ns) in sorted(disp.items(), key=lambda kv: kv[0][1]):
+        per.setdefault(name, []).append((cyc / 8 / ns * 1e3, ns))
+    print(f"{'kernel':<72} {'dispatches':>10} {'MHz':>7} {'avg_ns':>9}")
+    for name, v in per.items():
+        tail = v[len(v) // 2:]
+        print(f"{name[:72]:<72} {len(v):>10} {np.mean([x[0] for x in tail]):>7.0f} {np.mean([x[1] for x in tail]):>9.0f}")
 
 
 def trace_summary(path):
@@ -511,9 +540,16 @@ def main():
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     ap.add_argument("--trace-summary", metavar="CSV",
                     help="print per-(kernel, grid) statistics of a rocprofv3 kernel-trace CSV and exit")
+    ap.add_argument("--pmc-clock", metavar="CSV",
+                    help="print the shader clock per kernel from a rocprofv3 --pmc GRBM_GUI_ACTIVE CSV and exit")
+    ap.add_argument("--const-inputs", action="store_true",
+                    help="prefill leg only: q, k, v all 2^-7 (clock measurement; not a benchmark result)")
     args = ap.parse_args()
     if args.trace_summary:
         trace_summary(args.trace_summary)
+        return
+    if args.pmc_clock:
+        pmc_clock(args.pmc_clock)
         return
     if args.calib_copy:
         import torch
@@ -577,7 +613,10 @@ def main():
         return
 
     cfg = W.CONFIGS[2]
-    run2 = prep_qx(torch, ops, cfg)
+    if args.const_inputs and one != "prefill":
+        print("bench.py: --const-inputs applies to --only prefill", file=sys.stderr)
+        sys.exit(2)
+    run2 = prep_qx(torch, ops, cfg, const_inputs=args.const_inputs)
     if one == "prefill":
         wall, kms = bench_prefill(torch, run2, args.steps, args.warmup)
         print(json.dumps({"TFLOPs": round(cfg.flops() / wall / 1e12, 2), "kernel_ms": round(kms, 4)}), flush=True)
