@@ -19,11 +19,15 @@
 // on the matrix cores in the hardware's order, as the reference's tensor-core products do in theirs, so results
 // agree to bf16 accuracy, not bit for bit.
 //
-// Layout for MI355X: one workgroup of 4 wavefronts per (sequence, value head), as the reference's one CTA; every
-// product is a v_mfma_f32_32x32x16_bf16 sequence over LDS operands (A operands row-major, B operands stored
-// transposed so that both fragments are one 16-byte read per lane; rows XOR-swizzled in 16-byte units against bank
-// conflicts). The state lives in the accumulators of the wavefronts (32 k-dims each, 4 tiles of 32 x 32) and its
-// bf16 copy in LDS for the next chunk's products.
+// Layout for MI355X: one workgroup of 4 wavefronts per (sequence, value head), as the reference's one CTA, with the
+// 128 x 128 state in the accumulators: wavefront w owns v-dims 32 w .. 32 w + 31 of it. Every product is a
+// v_mfma_f32_32x32x16_bf16 sequence; the products that involve the state or the chunk's x = u - w h (w h, q h,
+// AQ vn, k^T vdec) take that operand straight from the wavefront's own accumulators (bf16 pairs and one
+// v_permlane32_swap per pair to reach the MFMA's k order), so the state never goes through LDS. A chunk's q, k, v
+// and A are copied from HBM straight into LDS (global_load_lds_dwordx4) one chunk ahead, into the other of two
+// buffer sets, so the copy overlaps the current chunk's products; operands whose k runs down the stored rows are
+// read with ds_read_b64_tr_b16, and products whose results feed other wavefronts are computed transposed where
+// that lets each lane store 4 adjacent bf16 at once. Two barriers per chunk.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -31,54 +35,87 @@
 #include "libreax_howu.h"
 #pragma GCC visibility pop
 
-#include "fmha_common.h"
+#include "fmha_tiles.h"
 
 namespace reax {
 namespace {
 
 constexpr int HW_BT = 64, HW_D = 128, HW_THREADS = 256;
 
-// element (r, c) of a row-major bf16 matrix W columns wide, 16-byte units XOR-swizzled by the row. Rows of 64
-// (128 bytes, two per 256-byte line of the 64 banks) also mix row / 8 into the XOR: fragment reads of 16
-// consecutive rows then use 16 distinct bank groups, and the transposed 2-byte stores of 16 rows 8 apart (the
-// staging of k^T, vb^T, kb^T) spread over 8 of them instead of one.
-template <int W>
-__device__ __forceinline__ int sw(int r, int c) {
-  const int f = W == 64 ? (r ^ (r >> 3)) & 7 : r & (W / 8 - 1);
-  return r * W + (((c >> 3) ^ f) << 3) + (c & 7);
-}
+// Row swizzles. 256-byte rows (q, k, v / vb, kb, wb): unit u of row r at ((u ^ swz(r)) << 4), the attention
+// kernels' K/V layout (fragment reads of 16 consecutive rows and transposed reads of 4 rows x 4 units are both
+// free of bank conflicts). 128-byte rows (A, AQ; two rows per 256-byte bank line): unit u of row r at
+// ((u ^ sw8(r)) << 4), which puts 16 consecutive rows' units in 16 distinct bank groups.
+__device__ __forceinline__ int sw8(int r) { return (r ^ (r >> 3)) & 7; }
+__device__ __forceinline__ int off256(int r, int u) { return r * 256 + ((u ^ swz(r)) << 4); }
+__device__ __forceinline__ int off128(int r, int u) { return r * 128 + ((u ^ sw8(r)) << 4); }
 
+// One chunk's inputs as copied from HBM (q, k, v rows of 128 bf16, A rows of 64) and its per-token scalars.
+struct HowuSet {
+  uint16_t q[HW_BT * HW_D];
+  uint16_t k[HW_BT * HW_D];
+  uint16_t v[HW_BT * HW_D];  // turned into vb = bf16(v beta) in place before the chunk's products
+  uint16_t a[HW_BT * HW_BT];
+  float g[HW_BT], eg[HW_BT], beta[HW_BT], da[HW_BT];  // g, 2^g, beta, 2^(g_last - g) (0 past the chunk's end)
+};
 struct HowuLds {
-  uint16_t q[HW_BT * HW_D];    // [t][d]
-  uint16_t k[HW_BT * HW_D];    // [s][d]: B^T of q k^T
-  uint16_t kt[HW_D * HW_BT];   // [d][t]: A of k^T vdec
-  uint16_t a[HW_BT * HW_BT];   // [t][s]
-  uint16_t vbt[HW_D * HW_BT];  // [c][s]: B^T of A vb; then vn^T
-  uint16_t kbt[HW_D * HW_BT];  // [c][s]: B^T of A kb; then vdec^T
-  uint16_t wb[HW_BT * HW_D];   // [t][d]
-  uint16_t hst[HW_D * HW_D];   // [c][d]: bf16(h)^T
+  HowuSet set[2];              // chunk i computes from set[i & 1] while chunk i + 1 is copied into the other
+  uint16_t kb[HW_BT * HW_D];   // [s][d] bf16(bf16(k beta) 2^g)
+  uint16_t wb[HW_BT * HW_D];   // [t][d] bf16(A kb); the norm epilogue stages o here
   uint16_t aq[HW_BT * HW_BT];  // [t][s]
-  float g[HW_BT], eg[HW_BT], beta[HW_BT], da[HW_BT];
 };
 
-__device__ __forceinline__ uint16_t bf16_bits(float x) { return (uint16_t)(pack_bf16x2(x, 0.f) & 0xffffu); }
-__device__ __forceinline__ float bf16_val(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+// Inputs past a sequence's end and A's blocks above the diagonal blocks are copied from here: 16 zero bytes.
+__device__ __align__(16) uint32_t howu_zero[4];
 
-// acc += A[m0.., k0..k0+16*KS) . B[k0.., n0..] with A row-major (AW wide) and B stored transposed (BW wide)
-template <int KS, int AW, int BW>
-__device__ __forceinline__ void mm(f32x16_t& acc, const uint16_t* A, int m0, const uint16_t* BT, int n0, int k0,
-                                   int lane) {
-  const int r = lane & 31, kh = 8 * (lane >> 5);
-#pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    const int kc = k0 + 16 * s + kh;
-    const bf16x8_t a = as_bf16x8(*reinterpret_cast<const u32x4_t*>(A + sw<AW>(m0 + r, kc)));
-    const bf16x8_t b = as_bf16x8(*reinterpret_cast<const u32x4_t*>(BT + sw<BW>(n0 + r, kc)));
-    acc = mfma32(a, b, acc);
-  }
+__device__ __forceinline__ float bf16_val(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+__device__ __forceinline__ float bf16_round(float x) { return __uint_as_float(pack_bf16x2(x, 0.f) << 16); }
+
+// Workgroup barrier once this wavefront's LDS accesses have completed, leaving its vector-memory operations (the
+// next chunk's copies, output stores) in flight.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// MFMA operand (a 32-wide block of m or n, 16 k) from LDS rows of 256 bytes: row `row` (the lane's m or n), the
+// lane's 8 consecutive k at unit 2 ks + (lane / 32).
+__device__ __forceinline__ bf16x8_t frag256(const uint16_t* buf, int row, int ks, int hf) {
+  return as_bf16x8(*reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint8_t*>(buf) + off256(row, 2 * ks + hf)));
 }
-// row within a 32 x 32 accumulator tile of element v of this lane (the column is lane & 31)
-__device__ __forceinline__ int trow(int v, int lane) { return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3); }
+__device__ __forceinline__ bf16x8_t frag128(const uint16_t* buf, int row, int ks, int hf) {
+  return as_bf16x8(*reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint8_t*>(buf) + off128(row, 2 * ks + hf)));
+}
+
+// MFMA operand whose k runs down the rows of a 256-byte-row buffer [k][x]: x = 32 db + lane % 32, k rows of step ks,
+// read with two ds_read_b64_tr_b16 (in each 16-lane group lane i reads 4 x-values of row i / 4 and receives row
+// 0..3's values of x-value i). NAT: lane half hf gets k = 16 ks + 8 hf + 0..7 (the MFMA's own k order); otherwise
+// k = 16 ks + 4 hf + {0..3, 8..11}, the order of a 32 x 32 accumulator's rows, so that the other operand can be taken
+// from accumulators as they are (any k order serves as long as both operands share it).
+template <bool NAT>
+__device__ __forceinline__ bf16x8_t tr_frag(const uint16_t* buf, int db, int ks, int lane) {
+  const int i = lane & 15, dh = (lane >> 4) & 1, hf = lane >> 5;
+  u32x2_t part[2];
+#pragma unroll
+  for (int sec = 0; sec < 2; ++sec) {
+    const int row = 16 * ks + (NAT ? 8 * hf + 4 * sec : 4 * hf + 8 * sec) + (i >> 2);
+    const int unit = 4 * db + 2 * dh + ((i >> 1) & 1);
+    part[sec] = ds_read_tr16(reinterpret_cast<const uint8_t*>(buf) + off256(row, unit) + 8 * (i & 1));
+  }
+  return as_bf16x8(u32x4_t{part[0][0], part[0][1], part[1][0], part[1][1]});
+}
+
+// MFMA operand over rows 16 s .. 16 s + 15 of a 32 x 32 fp32 accumulator tile (its rows are the operand's k, the
+// lane's column its m or n), rounded to bf16. NAT: in the MFMA's k order, which takes one exchange with the lane 32
+// away per register pair (v_permlane32_swap: lanes 0-31 hold rows 16 s + {0..3, 8..11}, lanes 32-63 rows
+// 16 s + {4..7, 12..15}); otherwise in the accumulator's own row order (pairs with tr_frag<false>).
+template <bool NAT>
+__device__ __forceinline__ bf16x8_t acc_frag(const f32x16_t& a, int s) {
+  const uint32_t p0 = pack_bf16x2(a[8 * s + 0], a[8 * s + 1]), p1 = pack_bf16x2(a[8 * s + 2], a[8 * s + 3]);
+  const uint32_t p2 = pack_bf16x2(a[8 * s + 4], a[8 * s + 5]), p3 = pack_bf16x2(a[8 * s + 6], a[8 * s + 7]);
+  if (!NAT) return as_bf16x8(u32x4_t{p0, p1, p2, p3});
+  const auto r0 = __builtin_amdgcn_permlane32_swap(p0, p2, false, false);
+  const auto r1 = __builtin_amdgcn_permlane32_swap(p1, p3, false, false);
+  return as_bf16x8(u32x4_t{r0[0], r1[0], r0[1], r1[1]});
+}
 
 // z / (1 + exp(-z)) in fp32 for the gated norm: |z| < 64 by 2^(-z log2 e) with the exponent split into an exact
 // 16-significant-bit product and a small remainder (second-order correction), about 5 ulp; otherwise with exp in
@@ -110,148 +147,265 @@ __global__ void __launch_bounds__(HW_THREADS, 1) howu_kernel(const uint16_t* __r
                                                              uint16_t* __restrict__ o, const int64_t* __restrict__ cu,
                                                              float scale, int NSEQ, int H, int HV, const NormArgs na) {
   __shared__ __align__(16) HowuLds S;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, jc = lane & 31;
-  const int i_n = NSEQ - 1 - (int)(blockIdx.x / HV), hv = (int)(blockIdx.x % HV), kh = hv / (HV / H);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, l32 = lane & 31, hf = lane >> 5;
+  // Workgroups are dealt to the 8 XCDs in turn (workgroup b to XCD b % 8). The GQ value heads of one key head are
+  // placed on one XCD, so that their shared q and k rows are read from HBM once and then hit that XCD's L2.
+  const int GQ = HV / H;
+  int item = (int)blockIdx.x;
+  if (GQ > 1) {
+    const int full = (NSEQ * HV) / (8 * GQ) * (8 * GQ);
+    if (item < full) item = (((item >> 3) / GQ) * 8 + (item & 7)) * GQ + (item >> 3) % GQ;
+  }
+  const int i_n = NSEQ - 1 - item / HV, hv = item % HV, kh = hv / GQ;
   const long long bos = cu[i_n];
   const int T = (int)(cu[i_n + 1] - bos);
-  // 64 x 128 products: wavefront wv owns rows 32 (wv >> 1).., columns 64 (wv & 1) + 32 tt (tt = 0, 1)
-  const int om0 = 32 * (wv >> 1), on0 = 64 * (wv & 1);
-  // the state: k-dims 32 wv.., v-dims 32 tt (tt = 0..3)
+  const int nch = (T + HW_BT - 1) / HW_BT;
+
+  // Copies: wavefront wv fills rows 16 wv .. 16 wv + 15 of q, k, v (four 1 KB direct-to-LDS loads each: rows
+  // 16 wv + 4 i + lane / 16) and of A (two loads: rows 16 wv + 8 i + lane / 8); lane l of a load lands at byte
+  // 16 l of it, i.e. at a swizzled unit of its row, and fetches the unit the swizzle puts there.
+  uint32_t off_qk[4], off_v[4], off_a[2];
+  int row_a[2], unit_a[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * wv + 4 * i + (lane >> 4), u = (lane & 15) ^ swz(r);
+    off_qk[i] = (uint32_t)(r * H * 256 + 16 * u);
+    off_v[i] = (uint32_t)(r * HV * 256 + 16 * u);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = 16 * wv + 8 * i + (lane >> 3), u = (lane & 7) ^ sw8(r);
+    row_a[i] = r;
+    unit_a[i] = u;
+    off_a[i] = (uint32_t)(r * HV * 128 + 16 * u);
+  }
+  const uint8_t* zero = reinterpret_cast<const uint8_t*>(howu_zero);
+  float g_next = 0.f, b_next = 0.f;  // g and beta of token `lane` of the chunk being copied
+
+  auto issue = [&](int c, HowuSet& st) {
+    const int t0 = c * HW_BT, nv = min(HW_BT, T - t0);
+    const uint8_t* qb = reinterpret_cast<const uint8_t*>(q + ((bos + t0) * H + kh) * HW_D);
+    const uint8_t* kb_ = reinterpret_cast<const uint8_t*>(k + ((bos + t0) * H + kh) * HW_D);
+    const uint8_t* vb_ = reinterpret_cast<const uint8_t*>(v + ((bos + t0) * HV + hv) * HW_D);
+    const uint8_t* ab = reinterpret_cast<const uint8_t*>(Ag + ((bos + t0) * HV + hv) * HW_BT);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = 16 * wv + 4 * i + (lane >> 4) < nv;
+      lds_dma16_asm<false>(ok ? qb + off_qk[i] : zero, reinterpret_cast<uint8_t*>(st.q) + (4 * wv + i) * 1024);
+      lds_dma16_asm<false>(ok ? kb_ + off_qk[i] : zero, reinterpret_cast<uint8_t*>(st.k) + (4 * wv + i) * 1024);
+      lds_dma16_asm<false>(ok ? vb_ + off_v[i] : zero, reinterpret_cast<uint8_t*>(st.v) + (4 * wv + i) * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      // the skip form reads A's blocks above the diagonal 16 x 16 blocks as zeros
+      const bool ok = row_a[i] < nv && (DENSE || (unit_a[i] >> 1) <= (row_a[i] >> 4));
+      lds_dma16_asm<false>(ok ? ab + off_a[i] : zero, reinterpret_cast<uint8_t*>(st.a) + (2 * wv + i) * 1024);
+    }
+    const bool ok = lane < nv;
+    const long long row = (bos + t0 + lane) * HV + hv;
+    g_next = ok ? g[row] : 0.f;
+    b_next = ok ? bf16_val(beta[row]) : 0.f;
+  };
+  // Once chunk c's copies have landed: its scalars, then vb = bf16(v beta) in place and kb = bf16(bf16(k beta) 2^g),
+  // each wavefront on the 16 rows it copied itself (so no barrier is needed between its copies and this pass).
+  auto prep = [&](int c, HowuSet& st) {
+    wait_vm();
+    const int nv = min(HW_BT, T - c * HW_BT);
+    const float glast = __shfl(g_next, nv - 1);
+    if ((lane >> 4) == wv) {
+      st.g[lane] = g_next;
+      st.eg[lane] = fast_exp2(g_next);
+      st.beta[lane] = b_next;
+      st.da[lane] = lane < nv ? fast_exp2(glast - g_next) : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 16 * wv + 4 * i + (lane >> 4), byte = r * 256 + 16 * (lane & 15);
+      const float b = st.beta[r], e = st.eg[r];
+      const u32x4_t vw = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint8_t*>(st.v) + byte);
+      const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint8_t*>(st.k) + byte);
+      u32x4_t vo, ko;
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        vo[x] = pack_bf16x2(bf16lo(vw[x]) * b, bf16hi(vw[x]) * b);
+        ko[x] = pack_bf16x2(bf16_round(bf16lo(kw[x]) * b) * e, bf16_round(bf16hi(kw[x]) * b) * e);
+      }
+      *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint8_t*>(st.v) + byte) = vo;
+      *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint8_t*>(S.kb) + byte) = ko;
+    }
+  };
+
+  // The state h [128 k-dims][128 v-dims]: wavefront wv holds v-dims 32 wv .. 32 wv + 31 of all k-dims, tile j =
+  // k-dims 32 j .. 32 j + 31 (accumulator layout: column = v-dim, rows = k-dims).
   f32x16_t h[4];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt)
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) h[tt][e] = 0.f;
-
-  for (int t0 = 0, it = 0; t0 < T; t0 += HW_BT, ++it) {
-    const int nv = min(HW_BT, T - t0);
-    // ---- stage the chunk: q, k (and k^T), A (lower block triangle unless DENSE), g, beta, then vb^T, kb^T
-    if (tid < HW_BT) {
-      const bool ok = tid < nv;
-      const long long row = (bos + t0 + tid) * HV + hv;
-      const float gg = ok ? g[row] : 0.f;
-      S.g[tid] = gg;
-      S.eg[tid] = fast_exp2(gg);
-      S.beta[tid] = ok ? bf16_val(beta[row]) : 0.f;
-    }
-    for (int i = tid; i < HW_BT * (HW_D / 8); i += HW_THREADS) {
-      const int t = i >> 4, c8 = (i & 15) * 8;
-      u32x4_t qw = {0u, 0u, 0u, 0u}, kw = {0u, 0u, 0u, 0u};
-      if (t < nv) {
-        const long long ro = ((bos + t0 + t) * H + kh) * HW_D + c8;
-        qw = *reinterpret_cast<const u32x4_t*>(q + ro);
-        kw = *reinterpret_cast<const u32x4_t*>(k + ro);
-      }
-      *reinterpret_cast<u32x4_t*>(S.q + sw<HW_D>(t, c8)) = qw;
-      *reinterpret_cast<u32x4_t*>(S.k + sw<HW_D>(t, c8)) = kw;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) S.kt[sw<HW_BT>(c8 + e, t)] = (uint16_t)(kw[e >> 1] >> (16 * (e & 1)));
-    }
-    for (int i = tid; i < HW_BT * (HW_BT / 8); i += HW_THREADS) {
-      const int t = i >> 3, c8 = (i & 7) * 8;
-      u32x4_t aw = {0u, 0u, 0u, 0u};
-      if (t < nv && (DENSE || (c8 >> 4) <= (t >> 4)))
-        aw = *reinterpret_cast<const u32x4_t*>(Ag + ((bos + t0 + t) * HV + hv) * HW_BT + c8);
-      *reinterpret_cast<u32x4_t*>(S.a + sw<HW_BT>(t, c8)) = aw;
-    }
-    __syncthreads();
-    for (int i = tid; i < HW_BT * (HW_D / 8); i += HW_THREADS) {
-      const int t = i >> 4, c8 = (i & 15) * 8;
-      u32x4_t vw = {0u, 0u, 0u, 0u};
-      if (t < nv) vw = *reinterpret_cast<const u32x4_t*>(v + ((bos + t0 + t) * HV + hv) * HW_D + c8);
-      const u32x4_t kw = *reinterpret_cast<const u32x4_t*>(S.k + sw<HW_D>(t, c8));
-      const float b = S.beta[t], e = S.eg[t];
-#pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        const float vv = (x & 1) ? bf16hi(vw[x >> 1]) : bf16lo(vw[x >> 1]);
-        const float kk = (x & 1) ? bf16hi(kw[x >> 1]) : bf16lo(kw[x >> 1]);
-        S.vbt[sw<HW_BT>(c8 + x, t)] = bf16_bits(vv * b);
-        S.kbt[sw<HW_BT>(c8 + x, t)] = bf16_bits(bf16_val(bf16_bits(kk * b)) * e);
-      }
-    }
-    __syncthreads();
-
-    // ---- u = A vb (kept as bf16 values), wb = bf16(A kb) -> LDS, AQ -> LDS
-    float ub[2][16];
+    for (int e = 0; e < 16; ++e) h[j][e] = 0.f;
+  u32x2_t opend[2][4];  // the last chunk's o (bf16), stored after the next chunk's copies are issued
+  int t0_prev = 0, nv_prev = 0;
+  auto store_o = [&]() {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      f32x16_t cu_ = {}, cw = {};
-      mm<4, HW_BT, HW_BT>(cu_, S.a, om0, S.vbt, on0 + 32 * tt, 0, lane);
-      mm<4, HW_BT, HW_BT>(cw, S.a, om0, S.kbt, on0 + 32 * tt, 0, lane);
+      const int t = 32 * tt + l32;
+      if (t < nv_prev) {
+        uint16_t* orow = o + ((bos + t0_prev + t) * HV + hv) * HW_D + 32 * wv + 4 * hf;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        ub[tt][e] = bf16_val(bf16_bits(cu_[e]));
-        S.wb[sw<HW_D>(om0 + trow(e, lane), on0 + 32 * tt + jc)] = bf16_bits(cw[e]);
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x2_t*>(orow + 8 * j) = opend[tt][j];
       }
     }
+  };
+
+  if (nch > 0) {
+    issue(0, S.set[0]);
+    prep(0, S.set[0]);
+  }
+  for (int c = 0; c < nch; ++c) {
+    HowuSet& st = S.set[c & 1];
+    const int t0 = c * HW_BT, nv = min(HW_BT, T - t0);
+    __syncthreads();  // chunk c's copies, scalars, vb and kb are visible; every wavefront is done with chunk c - 1
+    if (c + 1 < nch) issue(c + 1, S.set[(c + 1) & 1]);
+    if (!NORM && c > 0) store_o();
+
+    // ---- bf16(h) as MFMA operands: hb[kd] covers k-dims 16 kd .. 16 kd + 15 (B of w h, A of (q h)^T)
+    bf16x8_t hb[8];
+#pragma unroll
+    for (int kd = 0; kd < 8; ++kd) hb[kd] = acc_frag<true>(h[kd >> 1], kd & 1);
+
+    // ---- A as fragments: row t = 32 tt + l32, s = 16 ks + 8 hf + 0..7 (A of A vb, B of (A kb)^T). In the skip form
+    // rows 0..31 have no s >= 32.
+    constexpr int KS0 = DENSE ? 4 : 2;
+    bf16x8_t af[2][4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int ks = 0; ks < (tt ? 4 : KS0); ++ks) af[tt][ks] = frag128(st.a, 32 * tt + l32, ks, hf);
+
+    // ---- ub = bf16(A vb) for v-dims 32 wv.. (rows t, kept in registers)
+    f32x16_t ub[2];
     {
-      const int am0 = 32 * (wv >> 1), an0 = 32 * (wv & 1);
-      f32x16_t c = {};
-      if (an0 <= am0) mm<8, HW_D, HW_D>(c, S.q, am0, S.k, an0, 0, lane);
+      bf16x8_t vf[4];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int t = am0 + trow(e, lane), s = an0 + jc;
-        float y = 0.f;
-        if (s <= t && t < nv) y = c[e] * fast_exp2(S.g[t] - S.g[s]);
-        S.aq[sw<HW_BT>(t, s)] = bf16_bits(y);
+      for (int ks = 0; ks < 4; ++ks) vf[ks] = tr_frag<true>(st.v, wv, ks, lane);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        f32x16_t acc = {};
+#pragma unroll
+        for (int ks = 0; ks < (tt ? 4 : KS0); ++ks) acc = mfma32(af[tt][ks], vf[ks], acc);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ub[tt][e] = bf16_round(acc[e]);
       }
     }
-    const float glast = S.g[nv - 1];
-    if (tid < HW_BT) S.da[tid] = tid < nv ? fast_exp2(glast - S.g[tid]) : 0.f;
-    __syncthreads();
+    // ---- wb = bf16(A kb) for k-dims 32 wv.., computed transposed (rows d, column t) -> wb[t][d]
+    {
+      bf16x8_t kf[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kf[ks] = tr_frag<true>(S.kb, wv, ks, lane);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        f32x16_t acc = {};
+#pragma unroll
+        for (int ks = 0; ks < (tt ? 4 : KS0); ++ks) acc = mfma32(kf[ks], af[tt][ks], acc);
+        const int t = 32 * tt + l32;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint8_t*>(S.wb) + off256(t, 4 * wv + j) + 8 * hf) =
+              u32x2_t{pack_bf16x2(acc[4 * j], acc[4 * j + 1]), pack_bf16x2(acc[4 * j + 2], acc[4 * j + 3])};
+      }
+    }
+    // ---- AQ[t][s] = bf16((q_t . k_s) 2^(g_t - g_s)) for s <= t < nv, else 0: wavefronts 0-2 take the 32 x 32
+    // tiles (s-block, t-block) (0, 0), (0, 1), (1, 1), computed transposed (rows s, column t) -> aq[t][s]. The
+    // tile (1, 0) is all zeros and never read.
+    if (wv < 3) {
+      const int sb = wv == 2 ? 1 : 0, tb = wv == 0 ? 0 : 1;
+      f32x16_t acc = {};
+#pragma unroll
+      for (int kd = 0; kd < 8; ++kd)
+        acc = mfma32(frag256(st.k, 32 * sb + l32, kd, hf), frag256(st.q, 32 * tb + l32, kd, hf), acc);
+      const int t = 32 * tb + l32;
+      const float gt = st.g[t];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int s0 = 32 * sb + 8 * j + 4 * hf;
+        const f32x4_t gs = *reinterpret_cast<const f32x4_t*>(st.g + s0);
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (s0 + e <= t && t < nv) ? acc[4 * j + e] * fast_exp2(gt - gs[e]) : 0.f;
+        *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint8_t*>(S.aq) + off128(t, 4 * sb + j) + 8 * hf) =
+            u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+      }
+    }
+    lds_barrier();  // wb and AQ complete
 
-    // ---- vw = wb bf16(h), oi = q bf16(h); vn, vdec (transposed into the vb^T / kb^T buffers)
-    float oi[2][16];
+    // ---- vw = wb bf16(h) for v-dims 32 wv..; x = ub - vw; vn = bf16(x), vdec = bf16(x 2^(g_last - g_t))
+    bf16x8_t vnf[4], vdf[4];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      f32x16_t cvw = {}, coi = {};
-      if (it > 0) {
-        mm<8, HW_D, HW_D>(cvw, S.wb, om0, S.hst, on0 + 32 * tt, 0, lane);
-        mm<8, HW_D, HW_D>(coi, S.q, om0, S.hst, on0 + 32 * tt, 0, lane);
+      f32x16_t acc = {};
+#pragma unroll
+      for (int kd = 0; kd < 8; ++kd) acc = mfma32(frag256(S.wb, 32 * tt + l32, kd, hf), hb[kd], acc);
+      f32x16_t x, xd;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x4_t da = *reinterpret_cast<const f32x4_t*>(st.da + 32 * tt + 8 * j + 4 * hf);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          x[4 * j + e] = ub[tt][4 * j + e] - acc[4 * j + e];
+          xd[4 * j + e] = x[4 * j + e] * da[e];
+        }
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        oi[tt][e] = coi[e];
-        const int t = om0 + trow(e, lane), c = on0 + 32 * tt + jc;
-        const float x = ub[tt][e] - cvw[e];
-        S.vbt[sw<HW_BT>(c, t)] = bf16_bits(x);
-        S.kbt[sw<HW_BT>(c, t)] = bf16_bits(x * S.da[t]);
+      for (int s = 0; s < 2; ++s) {
+        vnf[2 * tt + s] = acc_frag<true>(x, s);
+        vdf[2 * tt + s] = acc_frag<false>(xd, s);
       }
     }
-    __syncthreads();
-
-    // ---- o = bf16(fma(AQ vn, scale, (oi eg) scale)); h = h 2^glast + k^T vdec
+    // ---- o^T (rows v-dims 32 wv.., column t) = scale (AQ vn)^T + scale 2^(g_t) (q bf16(h))^T
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      f32x16_t ci = {};
-      mm<4, HW_BT, HW_BT>(ci, S.aq, om0, S.vbt, on0 + 32 * tt, 0, lane);
+      f32x16_t oi = {}, av = {};
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int t = om0 + trow(e, lane), c = on0 + 32 * tt + jc;
-        const float r = __builtin_fmaf(ci[e], scale, (oi[tt][e] * S.eg[t]) * scale);
-        if (NORM)
-          S.wb[sw<HW_D>(t, c)] = bf16_bits(r);  // staged for the epilogue (wb is free after vw)
-        else if (t < nv)
-          o[((bos + t0 + t) * HV + hv) * HW_D + c] = bf16_bits(r);
+      for (int kd = 0; kd < 8; ++kd) oi = mfma32(hb[kd], frag256(st.q, 32 * tt + l32, kd, hf), oi);
+#pragma unroll
+      for (int ks = 0; ks < 2 * (tt + 1); ++ks) av = mfma32(vnf[ks], frag128(S.aq, 32 * tt + l32, ks, hf), av);
+      const float egt = st.eg[32 * tt + l32];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float r[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = __builtin_fmaf(av[4 * j + e], scale, (oi[4 * j + e] * egt) * scale);
+        opend[tt][j] = u32x2_t{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
       }
     }
-    const float gl = fast_exp2(glast);
+    t0_prev = t0;
+    nv_prev = nv;
+    // ---- h = h 2^(g_last) + k^T vdec
+    const float gl = fast_exp2(st.g[nv - 1]);
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
+    for (int j = 0; j < 4; ++j) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) h[tt][e] = h[tt][e] * gl;
-      mm<4, HW_BT, HW_BT>(h[tt], S.kt, 32 * wv, S.kbt, 32 * tt, 0, lane);
+      for (int e = 0; e < 16; ++e) h[j][e] = h[j][e] * gl;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) h[j] = mfma32(tr_frag<false>(st.k, j, ks, lane), vdf[ks], h[j]);
     }
-    __syncthreads();  // every read of this chunk's LDS is done (and the staged o rows are visible)
+
     if (NORM) {
+      lds_barrier();  // every wavefront is done reading wb
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint8_t*>(S.wb) + off256(32 * tt + l32, 4 * wv + j) + 8 * hf) =
+              opend[tt][j];
+      lds_barrier();
       // two rows per wavefront at a time, one per 32-lane half: lane l of a half holds columns 4l .. 4l+3
-      const int half = lane >> 5, l32 = lane & 31;
 #pragma unroll 1
       for (int i = 0; i < HW_BT / 8; ++i) {
-        const int t = 2 * (wv * (HW_BT / 8) + i) + half;
+        const int t = 2 * (wv * (HW_BT / 8) + i) + hf;
         const int R = t < nv ? na.f2s[bos + t0 + t] : -1;
         if (R < 0) continue;  // the same for the whole half
-        const u32x2_t xo = *reinterpret_cast<const u32x2_t*>(S.wb + sw<HW_D>(t, 4 * l32));
+        const u32x2_t xo =
+            *reinterpret_cast<const u32x2_t*>(reinterpret_cast<const uint8_t*>(S.wb) + off256(t, l32 >> 1) + 8 * (l32 & 1));
         const float x[4] = {bf16lo(xo[0]), bf16hi(xo[0]), bf16lo(xo[1]), bf16hi(xo[1])};
         float p = ((x[0] * x[0] + x[1] * x[1]) + x[2] * x[2]) + x[3] * x[3];
 #pragma unroll
@@ -265,21 +419,17 @@ __global__ void __launch_bounds__(HW_THREADS, 1) howu_kernel(const uint16_t* __r
         float res[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float y = bf16_val(bf16_bits(x[e] * rr));
-          const float y2 = bf16_val(bf16_bits(w[e] * y));
+          const float y = bf16_round(x[e] * rr);
+          const float y2 = bf16_round(w[e] * y);
           res[e] = y2 * silu_f32(zz[e]);
         }
         *reinterpret_cast<u32x2_t*>(o + ((long long)R * HV + hv) * HW_D + 4 * l32) =
             u32x2_t{pack_bf16x2(res[0], res[1]), pack_bf16x2(res[2], res[3])};
       }
     }
-    // bf16(h)^T for the next chunk: element (d, c) of the state at hst[c][d]
-#pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) S.hst[sw<HW_D>(32 * tt + jc, 32 * wv + trow(e, lane))] = bf16_bits(h[tt][e]);
-    // (the next chunk's staging writes other buffers; its first barrier orders these stores before their reads)
+    if (c + 1 < nch) prep(c + 1, S.set[(c + 1) & 1]);
   }
+  if (!NORM && nch > 0) store_o();
 }
 
 template <bool DENSE, bool NORM = false>

@@ -2,7 +2,8 @@
 ABI against the CPU oracle with the reference's bf16 rounding points and the same bf16 chunk-solve A: max error
 within 2^-6 and mean error within 2^-10 of the output scale (the matrix products accumulate in fp32 in the matrix
 cores' order, the oracle in double, so bf16 roundings of intermediates can differ by an ulp and carry through the
-state), every token row written, over varlen sequences with partial chunks and GQA ratios 1-3. The oracle itself
+state), every token row written, over varlen sequences with partial chunks and GQA ratios 1-3, including grids
+of 16+ workgroups, where the kernel groups a key head's value heads onto one XCD. The oracle itself
 equals the token-by-token gated delta rule when its roundings are dropped (tests/test_howu_oracle.py)."""
 import numpy as np
 import pytest
@@ -27,7 +28,9 @@ def _gpu():
 
 @pytest.mark.parametrize("lens,H,HV,dense,seed", [([64], 1, 2, False, 20), ([70, 130], 1, 2, False, 21),
                                                    ([5, 200, 64], 2, 4, False, 22), ([150, 1], 1, 3, False, 23),
-                                                   ([300], 4, 8, True, 24)])
+                                                   ([300], 4, 8, True, 24),
+                                                   ([70, 1, 130, 64, 5, 128, 33, 200], 1, 2, False, 25),
+                                                   ([100, 64, 3, 190, 64, 1, 77, 128], 2, 4, True, 26)])
 def test_howu_matches_oracle(lens, H, HV, dense, seed):
     from reax_fmha import ops
 
