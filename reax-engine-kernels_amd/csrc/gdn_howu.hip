@@ -75,6 +75,13 @@ __device__ __forceinline__ float bf16_round(float x) { return __uint_as_float(pa
 // next chunk's copies, output stores) in flight.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Direct global -> LDS copy of 16 bytes per lane (lane l's bytes land at lds + 16 l). Without a memory clobber the
+// compiler may move other LDS accesses across it: the destination buffer set is neither read nor written between
+// the copy and prep()'s wait, which does clobber memory.
+__device__ __forceinline__ void dma16(const void* src, uint8_t* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(lds));
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0));
+}
 
 // MFMA operand (a 32-wide block of m or n, 16 k) from LDS rows of 256 bytes: row `row` (the lane's m or n), the
 // lane's 8 consecutive k at unit 2 ks + (lane / 32).
@@ -180,31 +187,39 @@ __global__ void __launch_bounds__(HW_THREADS, 1) howu_kernel(const uint16_t* __r
     off_a[i] = (uint32_t)(r * HV * 128 + 16 * u);
   }
   const uint8_t* zero = reinterpret_cast<const uint8_t*>(howu_zero);
-  float g_next = 0.f, b_next = 0.f;  // g and beta of token `lane` of the chunk being copied
+  float g_next = 0.f;  // g and beta (bits) of token `lane` of the chunk being copied
+  uint16_t b_next = 0;
 
-  auto issue = [&](int c, HowuSet& st) {
+  // Chunk c's copies in four parts (0: q, 1: k, 2: v, 3: A, g and beta), issued at points spread over the current
+  // chunk's products: every workgroup reaches the same point at about the same time, and a burst of all of them
+  // held the issuing wavefronts for as long as HBM took to deliver it.
+  auto issue = [&](int c, HowuSet& st, int part) {
     const int t0 = c * HW_BT, nv = min(HW_BT, T - t0);
-    const uint8_t* qb = reinterpret_cast<const uint8_t*>(q + ((bos + t0) * H + kh) * HW_D);
-    const uint8_t* kb_ = reinterpret_cast<const uint8_t*>(k + ((bos + t0) * H + kh) * HW_D);
-    const uint8_t* vb_ = reinterpret_cast<const uint8_t*>(v + ((bos + t0) * HV + hv) * HW_D);
-    const uint8_t* ab = reinterpret_cast<const uint8_t*>(Ag + ((bos + t0) * HV + hv) * HW_BT);
+    if (part < 3) {
+      const uint16_t* src = part == 2 ? v + ((bos + t0) * HV + hv) * HW_D : (part ? k : q) + ((bos + t0) * H + kh) * HW_D;
+      uint16_t* dst = part == 2 ? st.v : part ? st.k : st.q;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool ok = 16 * wv + 4 * i + (lane >> 4) < nv;
-      lds_dma16_asm<false>(ok ? qb + off_qk[i] : zero, reinterpret_cast<uint8_t*>(st.q) + (4 * wv + i) * 1024);
-      lds_dma16_asm<false>(ok ? kb_ + off_qk[i] : zero, reinterpret_cast<uint8_t*>(st.k) + (4 * wv + i) * 1024);
-      lds_dma16_asm<false>(ok ? vb_ + off_v[i] : zero, reinterpret_cast<uint8_t*>(st.v) + (4 * wv + i) * 1024);
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = 16 * wv + 4 * i + (lane >> 4) < nv;
+        dma16(ok ? reinterpret_cast<const uint8_t*>(src) + (part == 2 ? off_v[i] : off_qk[i]) : zero,
+              reinterpret_cast<uint8_t*>(dst) + (4 * wv + i) * 1024);
+      }
+      return;
     }
+    const uint8_t* ab = reinterpret_cast<const uint8_t*>(Ag + ((bos + t0) * HV + hv) * HW_BT);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       // the skip form reads A's blocks above the diagonal 16 x 16 blocks as zeros
       const bool ok = row_a[i] < nv && (DENSE || (unit_a[i] >> 1) <= (row_a[i] >> 4));
-      lds_dma16_asm<false>(ok ? ab + off_a[i] : zero, reinterpret_cast<uint8_t*>(st.a) + (2 * wv + i) * 1024);
+      dma16(ok ? ab + off_a[i] : zero, reinterpret_cast<uint8_t*>(st.a) + (2 * wv + i) * 1024);
     }
-    const bool ok = lane < nv;
-    const long long row = (bos + t0 + lane) * HV + hv;
-    g_next = ok ? g[row] : 0.f;
-    b_next = ok ? bf16_val(beta[row]) : 0.f;
+    // g and beta of token `lane` (rows past the end read the last token's; prep() zeroes them). Unconditional
+    // loads whose results are first used after the copies have landed: a masked load or a conversion here would
+    // make the compiler wait for it, and the vector-memory counter only counts down in order, so that wait would
+    // also wait for every copy issued above.
+    const long long row = (bos + t0 + min(lane, nv - 1)) * HV + hv;
+    g_next = g[row];
+    b_next = beta[row];
   };
   // Once chunk c's copies have landed: its scalars, then vb = bf16(v beta) in place and kb = bf16(bf16(k beta) 2^g),
   // each wavefront on the 16 rows it copied itself (so no barrier is needed between its copies and this pass).
@@ -213,10 +228,12 @@ __global__ void __launch_bounds__(HW_THREADS, 1) howu_kernel(const uint16_t* __r
     const int nv = min(HW_BT, T - c * HW_BT);
     const float glast = __shfl(g_next, nv - 1);
     if ((lane >> 4) == wv) {
-      st.g[lane] = g_next;
-      st.eg[lane] = fast_exp2(g_next);
-      st.beta[lane] = b_next;
-      st.da[lane] = lane < nv ? fast_exp2(glast - g_next) : 0.f;
+      const bool ok = lane < nv;
+      const float gg = ok ? g_next : 0.f;
+      st.g[lane] = gg;
+      st.eg[lane] = fast_exp2(gg);
+      st.beta[lane] = ok ? bf16_val(b_next) : 0.f;
+      st.da[lane] = ok ? fast_exp2(glast - gg) : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -244,73 +261,62 @@ __global__ void __launch_bounds__(HW_THREADS, 1) howu_kernel(const uint16_t* __r
     for (int e = 0; e < 16; ++e) h[j][e] = 0.f;
   u32x2_t opend[2][4];  // the last chunk's o (bf16), stored after the next chunk's copies are issued
   int t0_prev = 0, nv_prev = 0;
-  auto store_o = [&]() {
+  auto store_o = [&](int tt) {  // rows 32 tt .. 32 tt + 31 of the last chunk's o
+    const int t = 32 * tt + (lane & 31);
+    if (t < nv_prev) {
+      uint16_t* orow = o + ((bos + t0_prev + t) * HV + hv) * HW_D + 32 * wv + 4 * hf;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int t = 32 * tt + l32;
-      if (t < nv_prev) {
-        uint16_t* orow = o + ((bos + t0_prev + t) * HV + hv) * HW_D + 32 * wv + 4 * hf;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x2_t*>(orow + 8 * j) = opend[tt][j];
-      }
+      for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x2_t*>(orow + 8 * j) = opend[tt][j];
     }
   };
 
   if (nch > 0) {
-    issue(0, S.set[0]);
+    for (int part = 0; part < 4; ++part) issue(0, S.set[0], part);
     prep(0, S.set[0]);
   }
   for (int c = 0; c < nch; ++c) {
     HowuSet& st = S.set[c & 1];
     const int t0 = c * HW_BT, nv = min(HW_BT, T - t0);
     __syncthreads();  // chunk c's copies, scalars, vb and kb are visible; every wavefront is done with chunk c - 1
-    if (c + 1 < nch) issue(c + 1, S.set[(c + 1) & 1]);
-    if (!NORM && c > 0) store_o();
+    // The lane index passes through an empty asm so that the compiler derives the per-lane LDS addresses here,
+    // where they are used, instead of holding ~100 of them in registers across the loop.
+    int ln = tid & 63;
+    asm volatile("" : "+v"(ln));
+    const int lane = ln, l32 = ln & 31, hf = ln >> 5;
+    const bool more = c + 1 < nch;
+    HowuSet& nx = S.set[(c + 1) & 1];
+    if (more) issue(c + 1, nx, 0);
 
-    // ---- bf16(h) as MFMA operands: hb[kd] covers k-dims 16 kd .. 16 kd + 15 (B of w h, A of (q h)^T)
-    bf16x8_t hb[8];
-#pragma unroll
-    for (int kd = 0; kd < 8; ++kd) hb[kd] = acc_frag<true>(h[kd >> 1], kd & 1);
-
-    // ---- A as fragments: row t = 32 tt + l32, s = 16 ks + 8 hf + 0..7 (A of A vb, B of (A kb)^T). In the skip form
-    // rows 0..31 have no s >= 32.
+    // ---- ub = bf16(A vb) for v-dims 32 wv.. (rows t, kept in registers) and wb = bf16(A kb) for k-dims 32 wv..,
+    // computed transposed (rows d, column t) -> wb[t][d]. Both take A's rows as fragments (row t = 32 tt + l32,
+    // s = 16 ks + 8 hf + 0..7); in the skip form rows 0..31 have no s >= 32.
     constexpr int KS0 = DENSE ? 4 : 2;
-    bf16x8_t af[2][4];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int ks = 0; ks < (tt ? 4 : KS0); ++ks) af[tt][ks] = frag128(st.a, 32 * tt + l32, ks, hf);
-
-    // ---- ub = bf16(A vb) for v-dims 32 wv.. (rows t, kept in registers)
     f32x16_t ub[2];
     {
-      bf16x8_t vf[4];
+      bf16x8_t vf[4], kf[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) vf[ks] = tr_frag<true>(st.v, wv, ks, lane);
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        f32x16_t acc = {};
-#pragma unroll
-        for (int ks = 0; ks < (tt ? 4 : KS0); ++ks) acc = mfma32(af[tt][ks], vf[ks], acc);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) ub[tt][e] = bf16_round(acc[e]);
+      for (int ks = 0; ks < 4; ++ks) {
+        vf[ks] = tr_frag<true>(st.v, wv, ks, lane);
+        kf[ks] = tr_frag<true>(S.kb, wv, ks, lane);
       }
-    }
-    // ---- wb = bf16(A kb) for k-dims 32 wv.., computed transposed (rows d, column t) -> wb[t][d]
-    {
-      bf16x8_t kf[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kf[ks] = tr_frag<true>(S.kb, wv, ks, lane);
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt) {
-        f32x16_t acc = {};
+        f32x16_t au = {}, aw = {};
 #pragma unroll
-        for (int ks = 0; ks < (tt ? 4 : KS0); ++ks) acc = mfma32(kf[ks], af[tt][ks], acc);
+        for (int ks = 0; ks < (tt ? 4 : KS0); ++ks) {
+          const bf16x8_t af = frag128(st.a, 32 * tt + l32, ks, hf);
+          au = mfma32(af, vf[ks], au);
+          aw = mfma32(kf[ks], af, aw);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) ub[tt][e] = bf16_round(au[e]);
         const int t = 32 * tt + l32;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           *reinterpret_cast<u32x2_t*>(reinterpret_cast<uint8_t*>(S.wb) + off256(t, 4 * wv + j) + 8 * hf) =
-              u32x2_t{pack_bf16x2(acc[4 * j], acc[4 * j + 1]), pack_bf16x2(acc[4 * j + 2], acc[4 * j + 3])};
+              u32x2_t{pack_bf16x2(aw[4 * j], aw[4 * j + 1]), pack_bf16x2(aw[4 * j + 2], aw[4 * j + 3])};
+        if (tt == 0 && !NORM && c > 0) store_o(0);
+        if (tt == 1 && more) issue(c + 1, nx, 1);
       }
     }
     // ---- AQ[t][s] = bf16((q_t . k_s) 2^(g_t - g_s)) for s <= t < nv, else 0: wavefronts 0-2 take the 32 x 32
@@ -337,20 +343,31 @@ __global__ void __launch_bounds__(HW_THREADS, 1) howu_kernel(const uint16_t* __r
     }
     lds_barrier();  // wb and AQ complete
 
-    // ---- vw = wb bf16(h) for v-dims 32 wv..; x = ub - vw; vn = bf16(x), vdec = bf16(x 2^(g_last - g_t))
+    // ---- vw = wb bf16(h) and (q bf16(h))^T for v-dims 32 wv.., one 16-deep slice of k-dims at a time: bf16(h) as
+    // an MFMA operand straight from the state's accumulators (B of w h, A of (q h)^T)
+    f32x16_t vw[2] = {}, oi[2] = {};
+#pragma unroll
+    for (int kd = 0; kd < 8; ++kd) {
+      if (kd == 2 && !NORM && c > 0) store_o(1);
+      if (kd == 5 && more) issue(c + 1, nx, 2);
+      const bf16x8_t hb = acc_frag<true>(h[kd >> 1], kd & 1);
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt) {
+        vw[tt] = mfma32(frag256(S.wb, 32 * tt + l32, kd, hf), hb, vw[tt]);
+        oi[tt] = mfma32(hb, frag256(st.q, 32 * tt + l32, kd, hf), oi[tt]);
+      }
+    }
+    // ---- x = ub - vw; vn = bf16(x), vdec = bf16(x 2^(g_last - g_t)) as operands of (AQ vn)^T and k^T vdec
     bf16x8_t vnf[4], vdf[4];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      f32x16_t acc = {};
-#pragma unroll
-      for (int kd = 0; kd < 8; ++kd) acc = mfma32(frag256(S.wb, 32 * tt + l32, kd, hf), hb[kd], acc);
       f32x16_t x, xd;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const f32x4_t da = *reinterpret_cast<const f32x4_t*>(st.da + 32 * tt + 8 * j + 4 * hf);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          x[4 * j + e] = ub[tt][4 * j + e] - acc[4 * j + e];
+          x[4 * j + e] = ub[tt][4 * j + e] - vw[tt][4 * j + e];
           xd[4 * j + e] = x[4 * j + e] * da[e];
         }
       }
@@ -360,12 +377,11 @@ __global__ void __launch_bounds__(HW_THREADS, 1) howu_kernel(const uint16_t* __r
         vdf[2 * tt + s] = acc_frag<false>(xd, s);
       }
     }
+    if (more) issue(c + 1, nx, 3);
     // ---- o^T (rows v-dims 32 wv.., column t) = scale (AQ vn)^T + scale 2^(g_t) (q bf16(h))^T
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      f32x16_t oi = {}, av = {};
-#pragma unroll
-      for (int kd = 0; kd < 8; ++kd) oi = mfma32(hb[kd], frag256(st.q, 32 * tt + l32, kd, hf), oi);
+      f32x16_t av = {};
 #pragma unroll
       for (int ks = 0; ks < 2 * (tt + 1); ++ks) av = mfma32(vnf[ks], frag128(S.aq, 32 * tt + l32, ks, hf), av);
       const float egt = st.eg[32 * tt + l32];
@@ -373,7 +389,7 @@ __global__ void __launch_bounds__(HW_THREADS, 1) howu_kernel(const uint16_t* __r
       for (int j = 0; j < 4; ++j) {
         float r[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = __builtin_fmaf(av[4 * j + e], scale, (oi[4 * j + e] * egt) * scale);
+        for (int e = 0; e < 4; ++e) r[e] = __builtin_fmaf(av[4 * j + e], scale, (oi[tt][4 * j + e] * egt) * scale);
         opend[tt][j] = u32x2_t{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
       }
     }
@@ -429,7 +445,10 @@ __global__ void __launch_bounds__(HW_THREADS, 1) howu_kernel(const uint16_t* __r
     }
     if (c + 1 < nch) prep(c + 1, S.set[(c + 1) & 1]);
   }
-  if (!NORM && nch > 0) store_o();
+  if (!NORM && nch > 0) {
+    store_o(0);
+    store_o(1);
+  }
 }
 
 template <bool DENSE, bool NORM = false>
