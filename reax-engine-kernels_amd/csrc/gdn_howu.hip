@@ -78,9 +78,14 @@ __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::
 // Direct global -> LDS copy of 16 bytes per lane (lane l's bytes land at lds + 16 l). Without a memory clobber the
 // compiler may move other LDS accesses across it: the destination buffer set is neither read nor written between
 // the copy and prep()'s wait, which does clobber memory.
+// NT adds the nontemporal hint, for data read exactly once (v and A; q and k serve two value heads).
+template <bool NT = false>
 __device__ __forceinline__ void dma16(const void* src, uint8_t* lds) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(lds));
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0));
+  if (NT)
+    asm volatile("global_load_lds_dwordx4 %0, off nt" ::"v"(src), "{m0}"(m0));
+  else
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0));
 }
 
 // MFMA operand (a 32-wide block of m or n, 16 k) from LDS rows of 256 bytes: row `row` (the lane's m or n), the
@@ -201,8 +206,11 @@ __global__ void __launch_bounds__(HW_THREADS, 1) howu_kernel(const uint16_t* __r
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const bool ok = 16 * wv + 4 * i + (lane >> 4) < nv;
-        dma16(ok ? reinterpret_cast<const uint8_t*>(src) + (part == 2 ? off_v[i] : off_qk[i]) : zero,
-              reinterpret_cast<uint8_t*>(dst) + (4 * wv + i) * 1024);
+        const uint8_t* from = ok ? reinterpret_cast<const uint8_t*>(src) + (part == 2 ? off_v[i] : off_qk[i]) : zero;
+        if (part == 2)
+          dma16<true>(from, reinterpret_cast<uint8_t*>(dst) + (4 * wv + i) * 1024);
+        else
+          dma16<false>(from, reinterpret_cast<uint8_t*>(dst) + (4 * wv + i) * 1024);
       }
       return;
     }
@@ -211,7 +219,7 @@ __global__ void __launch_bounds__(HW_THREADS, 1) howu_kernel(const uint16_t* __r
     for (int i = 0; i < 2; ++i) {
       // the skip form reads A's blocks above the diagonal 16 x 16 blocks as zeros
       const bool ok = row_a[i] < nv && (DENSE || (unit_a[i] >> 1) <= (row_a[i] >> 4));
-      dma16(ok ? ab + off_a[i] : zero, reinterpret_cast<uint8_t*>(st.a) + (2 * wv + i) * 1024);
+      dma16<true>(ok ? ab + off_a[i] : zero, reinterpret_cast<uint8_t*>(st.a) + (2 * wv + i) * 1024);
     }
     // g and beta of token `lane` (rows past the end read the last token's; prep() zeroes them). Unconditional
     // loads whose results are first used after the copies have landed: a masked load or a conversion here would
