@@ -8,15 +8,17 @@
 //           bf16 or fp32 (part_fp32)
 //
 // The reference selects one of 15 / 16 CUTLASS sm80 tile configurations by index, all with the same results; here
-// index 0 runs the tile that is fastest on large products (256 x 256) and index c > 0 the gfx950 tile (gemm_tile.h)
-// nearest to the threadblock shape of the reference's config c. All tiles give the same bits too, so a caller that
-// times every index and keeps the fastest still chooses among real alternatives. An unknown index returns 9, as in
-// the reference.
+// index 0 runs the tile that is fastest on large products (256 x 256, or 256 x 160 where that fills the CUs better)
+// and index c > 0 the gfx950 tile (gemm_tile.h) nearest to the threadblock shape of the reference's config c. All
+// tiles give the same bits too, so a caller that times every index and keeps the fastest still chooses among real
+// alternatives. An unknown index returns 9, as in the reference.
 // Shapes follow CUTLASS's can_implement for 8-wide bf16 accesses (code 1): positive sizes, K (kps) and the output
 // row stride multiples of 8; missing buffers and rows not 16-byte aligned also return 1 (the reference faults on
 // them). A failed launch returns 4, like the reference's trailing launch-error check.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <atomic>
 
 #pragma GCC visibility push(default)
 #if defined(REAX_LIB_PLAIN)
@@ -49,6 +51,8 @@ __global__ void __launch_bounds__(T::THREADS) gemm_kernel(const uint16_t* __rest
   typename T::Acc acc;
   T::mainloop(S, x, w, K, s * kext, (s + 1) * kext, M, N, m_blk, n_blk, acc);
 
+  // One output per lane per store: accumulating C^T instead (four adjacent outputs per lane, one 8- or 16-byte store
+  // each) measured 2-3% slower on every tile.
   const int lane = threadIdx.x & 63, wm = T::wm(), wn = T::wn();
   OutT* o = out + s * obs;
 #pragma unroll
@@ -76,15 +80,46 @@ int launch_tile(const void* x, const void* w, void* out, int M, int N, int K, in
   return hipGetLastError() == hipSuccess ? 0 : 4;
 }
 
+// Compute units of the device that owns the stream (cached per device; 0 if it cannot be queried).
+int stream_cus(void* stream) {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (stream ? hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev) != hipSuccess : hipGetDevice(&dev) != hipSuccess)
+    return 0;
+  if (dev < 0 || dev >= 64) return 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) return 0;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// Config index 0 (the 256 x 256 tile) takes the 256 x 160 tile instead when that takes less time by rounds of the
+// grid over the CUs times tile area over per-CU rate. The narrower tile reads more LDS fragments per MFMA (6 per 5
+// against 3 per 4) and measured 0.72 of the wide tile's rate per CU; it wins where the wide tile leaves CUs idle
+// (N = 2560, M = 4096: 160 tiles of 256 x 256 on 256 CUs against 256 of 256 x 160). All tiles give the same bits.
+int pick_wide(int M, int N, int S, void* stream) {
+  const int cus = stream_cus(stream);
+  if (cus <= 0) return gemm::kD256x256;
+  auto rounds = [&](int bm, int bn) {
+    return (((long long)(M + bm - 1) / bm) * ((N + bn - 1) / bn) * S + cus - 1) / cus;
+  };
+  const double t256 = (double)rounds(256, 256) * 256 * 256, t160 = (double)rounds(256, 160) * 256 * 160 / 0.72;
+  return t160 < t256 ? gemm::kD256x160 : gemm::kD256x256;
+}
+
 template <typename OutT>
 int launch(int tile, const void* x, const void* w, void* out, int M, int N, int K, int kext, int S, long long ldo,
            long long obs, void* stream) {
   if (kext % gemm::BK) tile = gemm::kT128x128;  // the ring tiles copy whole 64-deep slices only
+  else if (tile == gemm::kD256x256) tile = pick_wide(M, N, S, stream);
   switch (tile) {
     case gemm::kD128x128: return launch_tile<gemm::D128x128, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
     case gemm::kD256x128: return launch_tile<gemm::D256x128, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
     case gemm::kD128x256: return launch_tile<gemm::D128x256, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
     case gemm::kD256x256: return launch_tile<gemm::D256x256, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
+    case gemm::kD256x160: return launch_tile<gemm::D256x160, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
     default: return launch_tile<gemm::T128x128, OutT>(x, w, out, M, N, K, kext, S, ldo, obs, stream);
   }
 }

@@ -136,9 +136,10 @@ struct DmaTile {
   static constexpr int THREADS = 64 * NWM * NWN, NWAVES = NWM * NWN;
   static constexpr int BM = 32 * WTM * NWM, BN = 32 * WTN * NWN;
   static constexpr int XCH = BM / 8, CH = (BM + BN) / 8;  // 1 KB chunks of X, of the whole slice
-  static constexpr int CPW = CH / NWAVES;                  // chunks copied per wavefront per slice
-  static_assert(CPW * NWAVES == CH, "whole chunks per wavefront");
+  static constexpr int CPW = (CH + NWAVES - 1) / NWAVES;   // chunks copied per wavefront per slice (at most)
+  static constexpr bool EVEN = CPW * NWAVES == CH;         // otherwise the last wavefronts copy one fewer
   static_assert(NS == 2 || NS == 3, "two or three slices in the ring");
+  static_assert(EVEN || NS == 2, "the 3-slice ring's partial waits count whole chunks per wavefront");
 
   struct Lds {
     uint16_t xs[NS][BM * BK];
@@ -160,6 +161,7 @@ struct DmaTile {
 #pragma unroll
       for (int i = 0; i < CPW; ++i) {
         const int c = wv * CPW + i;
+        if (!EVEN && c >= CH) break;  // wavefront-uniform
         const bool isx = c < XCH;
         const int r = 8 * (isx ? c : c - XCH) + (lane >> 3);
         const int u = (lane & 7) ^ (r & 7);
@@ -228,10 +230,11 @@ using D128x128 = DmaTile<2, 2, 2, 2, 2>;      // 4 wavefronts, 64 KB
 using D256x128 = DmaTile<4, 2, 2, 2, 2>;      // 8 wavefronts of 64 x 64, 96 KB
 using D128x256 = DmaTile<2, 4, 2, 2, 2>;      // 8 wavefronts of 64 x 64, 96 KB
 using D256x256 = DmaTile<2, 4, 4, 2, 2>;      // 8 wavefronts of 128 x 64, 128 KB
-enum TileId : unsigned char { kT128x128 = 0, kD128x128 = 1, kD256x128 = 2, kD128x256 = 3, kD256x256 = 4 };
-constexpr const char* kTileNames[5] = {"mfma 128x128x64, 4 waves, register-staged", "mfma 128x128x64, 4 waves, LDS ring",
+using D256x160 = DmaTile<8, 1, 1, 5, 2>;      // 8 wavefronts of 32 x 160, 104 KB (fills 256 CUs where N = 2560)
+enum TileId : unsigned char { kT128x128 = 0, kD128x128 = 1, kD256x128 = 2, kD128x256 = 3, kD256x256 = 4, kD256x160 = 5 };
+constexpr const char* kTileNames[6] = {"mfma 128x128x64, 4 waves, register-staged", "mfma 128x128x64, 4 waves, LDS ring",
                                        "mfma 256x128x64, 8 waves, LDS ring", "mfma 128x256x64, 8 waves, LDS ring",
-                                       "mfma 256x256x64, 8 waves, LDS ring"};
+                                       "mfma 256x256x64, 8 waves, LDS ring", "mfma 256x160x64, 8 waves, LDS ring"};
 
 // XCD-aware tile order: hardware hands consecutive workgroups to the 8 XCDs in turn, so workgroup b runs on XCD
 // b % 8. When the tile count is a multiple of 8, each XCD is given a contiguous range of the tile sequence; the
