@@ -127,6 +127,12 @@ int launch(int tile, const void* x, const void* w, void* out, int M, int N, int 
 }  // namespace
 }  // namespace reax
 
+namespace reax {
+namespace {
+constexpr const char* kWideName = "mfma 256x256x64 (256x160x64 where that fills the CUs better), 8 waves, LDS ring";
+}  // namespace
+}  // namespace reax
+
 extern "C" {
 
 #if defined(REAX_LIB_PLAIN)
@@ -136,7 +142,9 @@ extern "C" {
 static const unsigned char kPlainTile[15] = {4, 2, 1, 3, 3, 2, 2, 3, 3, 1, 0, 2, 2, 1, 0};
 
 int reax_gemm_ncfg(void) { return 15; }
-const char* reax_gemm_cfgname(int c) { return (c >= 0 && c < 15) ? reax::gemm::kTileNames[kPlainTile[c]] : "?"; }
+const char* reax_gemm_cfgname(int c) {
+  return c == 0 ? reax::kWideName : (c > 0 && c < 15) ? reax::gemm::kTileNames[kPlainTile[c]] : "?";
+}
 
 int reax_gemm(int cfg, const void* x, const void* w, void* d, int M, int N, int K, int ldd, void* stream) {
   if (cfg < 0 || cfg >= 15) return 9;  // gemm_plain2.cu:56
@@ -153,7 +161,9 @@ int reax_gemm(int cfg, const void* x, const void* w, void* d, int M, int N, int 
 static const unsigned char kSlicesTile[16] = {4, 2, 1, 3, 1, 2, 3, 0, 1, 3, 0, 2, 1, 1, 0, 2};
 
 int reax_slices_ncfg(void) { return 16; }
-const char* reax_slices_cfgname(int c) { return (c >= 0 && c < 16) ? reax::gemm::kTileNames[kSlicesTile[c]] : "?"; }
+const char* reax_slices_cfgname(int c) {
+  return c == 0 ? reax::kWideName : (c > 0 && c < 16) ? reax::gemm::kTileNames[kSlicesTile[c]] : "?";
+}
 
 int reax_slices(int cfg, int part_fp32, const void* x, const void* w, void* p, int M, int N, int kps, int S, int K,
                 void* stream) {

@@ -162,8 +162,9 @@ def test_splitkv_workspace_size():
 
 
 def test_gemm_config_names_cover_the_tiles():
-    # every index names one of the gfx950 tiles; index 0 is the 256 x 256 ring tile in each library, and every tile
-    # is reachable from some index of each library (so a caller that times all indices tries each tile)
+    # every index names one of the gfx950 tiles; index 0 is the 256 x 256 ring tile in each library (plain and slices
+    # take the 256 x 160 one instead where that fills the CUs better), and every tile is reachable from some index of
+    # each library (so a caller that times all indices tries each tile)
     P, S, G = abi.plain(), abi.slices(), abi.gv()
     for name, fn, n in (("plain", P.reax_gemm_cfgname, 15), ("slices", S.reax_slices_cfgname, 16),
                         ("gv", G.reax_gv_cfgname, 20)):
