@@ -336,19 +336,31 @@ __global__ void __launch_bounds__(256, HD == 128 ? 2 : 1) fmha_fwd_kernel(const 
 // issues all of a step's loads, one after every fourth MFMA of its MFMA phase (measured: the 32 direct-to-LDS
 // loads of a step issued by all wavefronts at the start of the step held each of them up for ~480 clocks; spread
 // this way they cost group 0 ~45 clocks each, while its matrix core work continues).
+// Q and O cross between HBM and registers through LDS (8 KB per wavefront): the loads and stores of 32 rows
+// spread over 32 rows each (16 bytes per row per instruction) kept an item's prologue and epilogue at ~4 us each;
+// as 1 KB copies of four whole rows they are ~4% of config 2 faster. The Q copies and the first K tile go out
+// before the row limits are worked out.
 constexpr int PP_NW = 8;
-#ifndef REAX_PP_STAGES
-#define REAX_PP_STAGES 2
-#endif
+constexpr int PP_STAGES = 2;
 constexpr int PP_BM = 256;
 
 template <int MODE, int NS>
-__global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, int o_vec8) {
+__global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, int o_vec) {
   constexpr int HD = 128;
   using T = FwdTile<HD>;
-  static_assert(NS >= 2 && NS <= 4, "2..4 K/V stages");
-  __shared__ __align__(1024) uint8_t kring[NS][T::TILE];
-  __shared__ __align__(1024) uint8_t vring[NS][T::TILE];
+  static_assert(NS == 2, "two K/V stages: K(0) is the only tile the prologue loads, with Q");
+  // one block, the K/V ring first: its operand reads reach every stage with an instruction's 16-bit offset.
+  // qo: each wavefront's 32 rows, Q on the way in and O on the way out (row-major, 16-byte units swizzled by
+  // swz(row)), so that both move between HBM and LDS as whole rows, four per 1 KB copy
+  struct Lds {
+    uint8_t kring[NS][T::TILE];
+    uint8_t vring[NS][T::TILE];
+    uint8_t qo[PP_NW][32 * HD * 2];
+  };
+  __shared__ __align__(1024) Lds L;
+  auto& kring = L.kring;
+  auto& vring = L.vring;
+  auto& qo = L.qo;
   __shared__ int s_lim[PP_NW];
   __shared__ std::conditional_t<MODE == MODE_VARLEN, VarlenSched, char> vs;  // varlen item schedule
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hf = lane >> 5, lr = lane & 31;
@@ -383,6 +395,39 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   const bool rvalid = r < Mb;
   const int tok = rvalid ? r / p.G : 0;
   const int g = rvalid ? r - tok * p.G : 0;
+  bf16x8_t qf[T::QK];
+  const uint16_t* Kb = p.k + (long long)b * p.ksB + (long long)hk * p.ksH + tok0 * p.ksM;
+  const uint16_t* Vb = p.v + (long long)b * p.vsB + (long long)hk * p.vsH + tok0 * p.vsM;
+  const uint16_t* qb = p.q + (long long)b * p.qsB + (long long)hk * p.qsH + tok0 * p.qsT;
+  {
+    // load i: lane l fetches row lrow = 4i + l/16 of the wavefront's 32 (token tq, head gq; rows past the tile's
+    // end read its last row), logical unit (l % 16) ^ swz(lrow)
+    const int lrow0 = lane >> 4, pu = lane & 15;
+    const int row0 = r0 + 32 * w + lrow0;
+    int tq = row0 / p.G, gq = row0 - tq * p.G;
+    const int d4 = 4 / p.G, m4 = 4 - d4 * p.G;
+    const int ltok = (Mb - 1) / p.G, lg = Mb - 1 - ltok * p.G;
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(&qo[w][0]));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = r0 + 32 * w + 4 * i + lrow0;
+      const bool ok = row < Mb;
+      const int u = pu ^ swz(4 * i + lrow0);
+      const uint16_t* src = qb + (long long)(ok ? tq : ltok) * p.qsT + (long long)(ok ? gq : lg) * p.qsG + 8 * u;
+      asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0 + i * 1024) : "memory");
+      tq += d4;
+      gq += m4;
+      if (gq >= p.G) { gq -= p.G; ++tq; }
+    }
+  }
+  const Dma<HD, PP_NW / 2> kplan(p.ksM, w, lane), vplan(p.vsM, w, lane);  // used by group 0 only
+  const bool kfast = p.ksM * 2 * T::BN < (1ll << 31), vfast = p.vsM * 2 * T::BN < (1ll << 31);
+  // the first K tile goes out with Q (an item whose rows see no key only wastes it)
+  if (grp == 0 && Nb > 0) {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));  // per-lane terms formed here, not hoisted out of the item loop
+    kplan.template tile<1>(kring[0], Kb, p.ksM, kfast, 0, Nb, (int)wu, ln);
+  }
   int lim = -1;
   if (rvalid) {
     lim = MODE == MODE_QPOS ? min(p.qpos[(long long)b * p.qpBs + tok], Nb - 1) : min(tok, Nb - 1);
@@ -392,19 +437,24 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   // they must not force the mask pass onto every key tile of a partial row tile.
   const int wmax = wave_max(lim), wmin = wave_min(rvalid ? lim : INT_MAX);
   if (lane == 0) s_lim[w] = wmax;
+  // the Q and K(0) copies are inline assembly, which the compiler does not count: wait for them explicitly
+  // (the barrier's own fence only drains the loads it knows of)
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
   int cmax = s_lim[0];
 #pragma unroll
   for (int i = 1; i < PP_NW; ++i) cmax = max(cmax, s_lim[i]);
   const int t_end = cmax < 0 ? 0 : cmax / T::BN + 1;
-
-  const uint16_t* qrow = p.q + (long long)b * p.qsB + (long long)hk * p.qsH + (tok0 + tok) * p.qsT + (long long)g * p.qsG;
-  bf16x8_t qf[T::QK];
+  // the wait and barrier above: this wavefront's Q copies and group 0's K(0) copies have landed
+  {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));  // addresses formed here, not kept live from the kernel's start
+    const uint32_t qa = (uint32_t)reinterpret_cast<uintptr_t>(&qo[w][0]) + k_lane_base<HD>(0, ln & 31, ln >> 5);
 #pragma unroll
-  for (int ks = 0; ks < T::QK; ++ks)
-    qf[ks] = as_bf16x8(rvalid ? ld16(qrow + 16 * ks + 8 * hf) : u32x4_t{0u, 0u, 0u, 0u});
-  const uint16_t* Kb = p.k + (long long)b * p.ksB + (long long)hk * p.ksH + tok0 * p.ksM;
-  const uint16_t* Vb = p.v + (long long)b * p.vsB + (long long)hk * p.vsH + tok0 * p.vsM;
+    for (int ks = 0; ks < T::QK; ++ks)
+      qf[ks] = as_bf16x8(*reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(qa ^ (32u * ks)));
+  }
+
 
   f32x16_t o[T::DB];
 #pragma unroll
@@ -416,8 +466,6 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   f32x16_t s[2];
   uint32_t pk[2][8];
 
-  const Dma<HD, PP_NW / 2> kplan(p.ksM, w, lane), vplan(p.vsM, w, lane);  // used by group 0 only
-  const bool kfast = p.ksM * 2 * T::BN < (1ll << 31), vfast = p.vsM * 2 * T::BN < (1ll << 31);
   const uint32_t kbase[2] = {k_lane_base<HD>(0, lr, hf), k_lane_base<HD>(1, lr, hf)};
   const uint32_t vbase = v_lane_base<HD>(lane);
 
@@ -545,16 +593,6 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
     // every load (DW = 4 per tile and wavefront); group 1 none.
     constexpr int PER_STEP = 2 * Dma<HD, PP_NW / 2>::DW;  // loads per group-0 wavefront per step
     static_assert(Dma<HD, PP_NW / 2>::DW == 4, "dma(j): j = 0..3 the K tile's loads, 4..7 the V tile's");
-    if (grp == 0) {
-#pragma unroll
-      for (int j = 0; j < NS - 1; ++j)
-        if (j < t_end) kplan.template tile<1>(kring[j], Kb, p.ksM, kfast, j * T::BN, Nb, w, lane);
-#pragma unroll
-      for (int j = 0; j < NS - 2; ++j)
-        if (j < t_end) vplan.template tile<1>(vring[j], Vb, p.vsM, vfast, j * T::BN, Nb, w, lane);
-    }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // all prologue loads (simplest: the first step needs K(0) anyway)
-    __syncthreads();
     auto step = [&](int t, const uint8_t* kb_t, uint8_t* kb_fill, const uint8_t* vb_prev, uint8_t* vb_fill) __attribute__((always_inline)) {
       // Group 0's loads of this step: K(t+NS-1) and V(t+NS-2). When both are whole tiles with 32-bit row offsets
       // (every step but the last one or two), each load is a per-lane offset added to a scalar tile base, issued
@@ -619,12 +657,49 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   // ---- epilogue: normalise, LSE, store
   const float l = halves_sum(l_run);
   const float inv = l > 0.f ? 1.0f / l : 0.f;
-  if (!rvalid) return;
-  if (p.lse && hf == 0) {
+  if (p.lse && rvalid && hf == 0) {
+    int re = r;
+    asm volatile("" : "+v"(re));  // the row's (token, head) recomputed here rather than kept across the loop
+    const int te = re / p.G, ge = re - te * p.G;
     const float lse = l > 0.f ? (m_run + log2f(l)) * 0.69314718055994530942f : -INFINITY;
-    p.lse[(long long)b * p.lsB + (long long)hk * p.lsH + (tok0 + tok) * p.lsT + (long long)g * p.lsG] = lse;
+    p.lse[(long long)b * p.lsB + (long long)hk * p.lsH + (tok0 + te) * p.lsT + (long long)ge * p.lsG] = lse;
   }
   if (!p.o) return;
+  if (o_vec == 2) {
+    // through qo[w]: lane (lr, hf) writes 8 bytes of row lr per (db, q4); lane l then reads 16 bytes of row
+    // 4i + l/16 and stores them: each store covers four whole rows
+    uint8_t* ob = &qo[w][0];
+    int ln = lane;
+    asm volatile("" : "+v"(ln));  // addresses formed here, not kept live across the key loop
+    const int lr2 = ln & 31, hf2 = ln >> 5;
+    const uint32_t wa = (uint32_t)reinterpret_cast<uintptr_t>(ob) + lr2 * 256 + 8 * hf2, sw = swz(lr2);
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const uint32_t w0 = pack_bf16x2(o[db][4 * q4 + 0] * inv, o[db][4 * q4 + 1] * inv);
+        const uint32_t w1 = pack_bf16x2(o[db][4 * q4 + 2] * inv, o[db][4 * q4 + 3] * inv);
+        *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(wa + ((((uint32_t)(4 * db + q4)) ^ sw) << 4)) =
+            u32x2_t{w0, w1};
+      }
+    uint16_t* obase = p.o + (long long)b * p.osB + (long long)hk * p.osH + tok0 * p.osT;
+    const int lrow0 = ln >> 4, pu = ln & 15;
+    const int row0 = r0 + 32 * w + lrow0;
+    int tq = row0 / p.G, gq = row0 - tq * p.G;
+    const int d4 = 4 / p.G, m4 = 4 - d4 * p.G;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(ob + i * 1024 + 16 * lane);
+      const int row = r0 + 32 * w + 4 * i + lrow0;
+      const int u = pu ^ swz(4 * i + lrow0);
+      if (row < Mb) *reinterpret_cast<u32x4_t*>(obase + (long long)tq * p.osT + (long long)gq * p.osG + 8 * u) = x;
+      tq += d4;
+      gq += m4;
+      if (gq >= p.G) { gq -= p.G; ++tq; }
+    }
+    return;
+  }
+  if (!rvalid) return;
   uint16_t* orow = p.o + (long long)b * p.osB + (long long)hk * p.osH + (tok0 + tok) * p.osT + (long long)g * p.osG;
 #pragma unroll
   for (int db = 0; db < T::DB; ++db)
@@ -633,7 +708,7 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
       const int d = 32 * db + 8 * q4 + 4 * hf;
       const uint32_t w0 = pack_bf16x2(o[db][4 * q4 + 0] * inv, o[db][4 * q4 + 1] * inv);
       const uint32_t w1 = pack_bf16x2(o[db][4 * q4 + 2] * inv, o[db][4 * q4 + 3] * inv);
-      if (o_vec8) {
+      if (o_vec) {
         *reinterpret_cast<u32x2_t*>(orow + d) = u32x2_t{w0, w1};
       } else {
         *reinterpret_cast<uint32_t*>(orow + d) = w0;
@@ -983,8 +1058,11 @@ static int launch_fwd_pp(FwdParams p, hipStream_t stream) {
   const int cus = device_cus(stream);
   if (cus <= 0) return (int)hipErrorInvalidDevice;
   const long long nwg = n_items < cus ? n_items : cus;  // one workgroup per CU (its LDS and registers fill one)
-  const int o_vec8 = p.o ? (aligned_elems(p.o, 4, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0) : 0;
-  hipLaunchKernelGGL((fmha_fwd_pp_kernel<MODE, REAX_PP_STAGES>), dim3((unsigned)nwg), dim3(64 * PP_NW), 0, stream, p, o_vec8);
+  // output stores: 2 whole rows staged through LDS (16-byte aligned rows), 1 eight-byte, 0 four-byte pieces
+  const int o_vec = !p.o ? 0
+                    : aligned_elems(p.o, 8, {p.osB, p.osH, p.osT, p.osG}) ? 2
+                    : aligned_elems(p.o, 4, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0;
+  hipLaunchKernelGGL((fmha_fwd_pp_kernel<MODE, PP_STAGES>), dim3((unsigned)nwg), dim3(64 * PP_NW), 0, stream, p, o_vec);
   return (int)hipGetLastError();
 }
 

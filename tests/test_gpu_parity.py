@@ -160,6 +160,27 @@ def test_qx_persistent_multi_item(B, S, Hq, Hkv):
     assert np.isfinite(W.bf16_bits_to_f32(og)).all()
 
 
+# The head_dim-128 prefill kernel picks its output store by the output's alignment: rows 16-byte aligned go out as
+# whole rows staged through LDS, 8-byte aligned ones as 8-byte pieces, the rest as 4-byte pieces. An output view
+# into rows padded by `pad` elements selects each; the padding must stay untouched.
+@pytest.mark.parametrize("pad", [8, 4, 2], ids=["rows16", "rows8", "rows4"])
+def test_qx_output_strides(pad):
+    from reax_fmha import ops
+
+    c = FC.Case(f"ostride_pad{pad}", B=2, S=120, N=120, Hq=8, Hkv=2, D=128, mode="causal", seed=41 + pad)
+    _say(f"qx output rows padded by {pad}")
+    a = FC.build(c)
+    q, k, v = dev(a["q"]), dev(a["k"]), dev(a["v"])
+    qpos = torch.from_numpy(a["qpos"]).cuda()
+    buf = torch.full((c.B, c.S, c.Hq, c.D + pad), -7.0, dtype=torch.bfloat16, device="cuda")
+    o = buf[..., : c.D]
+    _, lse = ops.attention(q, k, v, qpos, scale=c.scale, o=o)
+    torch.cuda.synchronize()
+    assert (buf[..., c.D:] == -7.0).all(), "padding written"
+    o_ref, lse_ref = FC.oracle_ref(c, a)
+    FC.check_tolerance(host(o.contiguous()), o_ref, lse.cpu().numpy(), lse_ref, where=c.name)
+
+
 GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
 
 
@@ -394,6 +415,19 @@ def test_varlen_ragged(seqlens, D):
     og, lg = run_varlen(c, a)
     o, lse = FC.oracle_ref(c, a)
     FC.check_tolerance(og, o, lg, lse, where="varlen")
+
+
+# Sequences of whole 256-row tiles (G = 4: 64 tokens a tile) in several sequences, so every wavefront of the
+# prefill kernel reads its Q rows back from LDS with no row past a tile's end: a read that overtook the copies
+# of its last rows showed up here as wrong rows 24..31 of the second wavefront group.
+def test_varlen_full_tiles():
+    c = FC.Case("varlen_full_tiles", B=1, S=0, N=0, Hq=8, Hkv=2, D=128, mode="varlen", seed=73,
+                seqlens=[64, 64, 192, 128, 64, 320])
+    _say(f"varlen full tiles {c.seqlens}")
+    a = FC.build(c)
+    og, lg = run_varlen(c, a)
+    o, lse = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, o, lg, lse, where="varlen_full_tiles")
 
 
 def test_config3_varlen():
