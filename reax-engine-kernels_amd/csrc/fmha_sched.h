@@ -21,6 +21,8 @@
 // Shapes beyond the LDS tables (VS_NSEQ sequences, VS_NPAIR pairs per class, VS_TMAX tiles per sequence,
 // VS_PMAX workgroups, VS_RMAX rounds) keep the fixed order.
 #pragma once
+#include <climits>
+
 #include "fmha_common.h"
 
 namespace reax {
@@ -34,7 +36,7 @@ struct VarlenSched {
   int pref[VS_NPAIR + 1];  // prefix sums of the class's pair item counts
   int cnt[VS_TMAX];        // the class's pairs with more than i items (they reach level i)
   int start[VS_TMAX];      // first position of level i in the class's item order
-  int load[VS_PMAX];       // work held by each workgroup of the class (half tile-steps)
+  alignas(16) int load[VS_PMAX];  // work held by each workgroup of the class (half tile-steps; INT_MAX past pw)
   int mine[VS_RMAX];       // this workgroup's item position in round r, -1 for none
   int ok, nx, tmax, nreal, rounds, npc;
 };
@@ -77,10 +79,11 @@ __device__ void vs_build(VarlenSched& S, const int* cu, int nseq, int H, int G, 
     return;
   }
   const int nx = (P % 8 == 0) ? 8 : 1, x = wg % nx, pw = P / nx, me = wg / nx;
-  // items per sequence, staged in cnt[] (VS_TMAX >= VS_NSEQ)
+  // items and tokens per sequence, staged in cnt[] and start[] (VS_TMAX >= VS_NSEQ): cu_seqlens is read once
   for (int s = tid; s < nseq; s += nt) {
     const int L = cu[s + 1] - cu[s];
     S.cnt[s] = L > 0 ? (int)(((long long)L * G + BM - 1) / BM) : 0;
+    S.start[s] = L;
   }
   __syncthreads();
   for (int s = tid; s < nseq; s += nt) {
@@ -92,7 +95,7 @@ __device__ void vs_build(VarlenSched& S, const int* cu, int nseq, int H, int G, 
     }
     S.sorted[r] = s;
     S.Ts[r] = T;
-    S.Ls[r] = cu[s + 1] - cu[s];
+    S.Ls[r] = S.start[s];
   }
   __syncthreads();
   if (tid == 0) {
@@ -133,7 +136,7 @@ __device__ void vs_build(VarlenSched& S, const int* cu, int nseq, int H, int G, 
     const int c = i + 1 < tmax ? S.cnt[i + 1] : 0;
     S.start[i] = S.pref[c] - c * (i + 1);
   }
-  for (int m = tid; m < pw; m += nt) S.load[m] = 0;
+  for (int m = tid; m < VS_PMAX; m += nt) S.load[m] = m < pw ? 0 : INT_MAX;
   for (int r = tid; r < VS_RMAX; r += nt) S.mine[r] = -1;
   __syncthreads();
   for (int r = 0; r < S.rounds; ++r) {
@@ -141,10 +144,21 @@ __device__ void vs_build(VarlenSched& S, const int* cu, int nseq, int H, int G, 
     const int m = tid;
     if (m < pw) {
       const int lm = S.load[m];
+      // rank of this workgroup's load: 16 loads per pass, read four at a time so the reads overlap (entries past
+      // pw hold INT_MAX and never count)
       int rk = 0;
-      for (int u = 0; u < pw; ++u) {
-        const int lu = S.load[u];
-        rk += (lu < lm || (lu == lm && u < m)) ? 1 : 0;
+      for (int u0 = 0; u0 < pw; u0 += 16) {
+        int4 q[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = *reinterpret_cast<const int4*>(&S.load[u0 + 4 * j]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int u = u0 + 4 * j;
+          rk += (q[j].x < lm || (q[j].x == lm && u + 0 < m)) ? 1 : 0;
+          rk += (q[j].y < lm || (q[j].y == lm && u + 1 < m)) ? 1 : 0;
+          rk += (q[j].z < lm || (q[j].z == lm && u + 2 < m)) ? 1 : 0;
+          rk += (q[j].w < lm || (q[j].w == lm && u + 3 < m)) ? 1 : 0;
+        }
       }
       const int k = r * pw + rk;
       if (k < S.nreal) {
