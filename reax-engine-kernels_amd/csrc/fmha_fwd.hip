@@ -687,12 +687,16 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
     const int row0 = r0 + 32 * w + lrow0;
     int tq = row0 / p.G, gq = row0 - tq * p.G;
     const int d4 = 4 / p.G, m4 = 4 - d4 * p.G;
+    // all eight reads first, so their LDS latencies overlap
+    u32x4_t x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = *reinterpret_cast<const u32x4_t*>(ob + i * 1024 + 16 * lane);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const u32x4_t x = *reinterpret_cast<const u32x4_t*>(ob + i * 1024 + 16 * lane);
       const int row = r0 + 32 * w + 4 * i + lrow0;
       const int u = pu ^ swz(4 * i + lrow0);
-      if (row < Mb) *reinterpret_cast<u32x4_t*>(obase + (long long)tq * p.osT + (long long)gq * p.osG + 8 * u) = x;
+      if (row < Mb) *reinterpret_cast<u32x4_t*>(obase + (long long)tq * p.osT + (long long)gq * p.osG + 8 * u) = x[i];
       tq += d4;
       gq += m4;
       if (gq >= p.G) { gq -= p.G; ++tq; }
