@@ -20,6 +20,9 @@
 #include <stdint.h>
 
 #include "fmha_common.h"
+#include "fmha_tiles.h"
+
+#include <type_traits>
 
 namespace reax {
 namespace gemm {
@@ -150,9 +153,108 @@ struct DmaTile {
   __device__ static int wm() { return 32 * WTM * ((int)(threadIdx.x >> 6) / NWN); }
   __device__ static int wn() { return 32 * WTN * ((int)(threadIdx.x >> 6) % NWN); }
 
+  __device__ __forceinline__ static void mainloop_pinned(Lds& S, const uint16_t* __restrict__ x,
+                                                  const uint16_t* __restrict__ w, long long ldx, int k0, int k1,
+                                                  int M, int N, int m_blk, int n_blk, Acc& acc) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm0 = wm(), wn0 = wn();
+    // copy i (of this wavefront's CPW) of slice kb into ring slot st: chunk wv * CPW + i
+    auto copy_one = [&](int st, int kb, int i) __attribute__((always_inline)) {
+      const int c = wv * CPW + i;
+      if (!EVEN && c >= CH) return;  // wavefront-uniform
+      const bool isx = c < XCH;
+      const int r = 8 * (isx ? c : c - XCH) + (lane >> 3);
+      const int u = (lane & 7) ^ (r & 7);
+      const int row = isx ? min(m_blk + r, M - 1) : min(n_blk + r, N - 1);
+      const uint16_t* src = (isx ? x : w) + (long long)row * ldx + kb + 8 * u;
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+          (uint32_t)reinterpret_cast<uintptr_t>(isx ? &S.xs[st][c * 512] : &S.ws[st][(c - XCH) * 512]));
+      asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+    };
+    // The slice multiply in a fixed issue order: one slot per MFMA (NM = 4 WTM WTN per slice, 16-deep step major,
+    // then a, b), scheduling barriers between slots. Step ks + 1's fragments are read during step ks (read q of
+    // R = WTM + WTN in slot q G / R of the step's G = WTM WTN slots, W's first), and the copies of a later slice go out one
+    // every NM / CPW slots: neither the reads nor the copies come in a burst that holds the matrix core up.
+    constexpr int G = WTM * WTN, R = WTM + WTN, NKS = BK / 16, NM = NKS * G;
+    auto compute = [&](int st, auto&& cp) __attribute__((always_inline)) {
+      const int r = lane & 31, hsel = lane >> 5;
+      bf16x8_t fr[2][R];
+      auto read = [&](auto ksc, auto qc) __attribute__((always_inline)) {
+        constexpr int ks = decltype(ksc)::value, q = decltype(qc)::value;
+        const int u = 2 * ks + hsel;
+        if constexpr (q < WTM)
+          fr[ks & 1][q] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&S.xs[st][slot(wm0 + 32 * q + r, u)]));
+        else
+          fr[ks & 1][q] = as_bf16x8(*reinterpret_cast<const u32x4_t*>(&S.ws[st][slot(wn0 + 32 * (q - WTM) + r, u)]));
+      };
+      static_for<0, R>([&](auto qc) __attribute__((always_inline)) { read(std::integral_constant<int, 0>{}, qc); });
+      __builtin_amdgcn_sched_barrier(0);
+      static_for<0, NM>([&](auto ic) __attribute__((always_inline)) {
+        constexpr int i = decltype(ic)::value;
+        constexpr int ks = i / G, j = i % G, a = j / WTN, b = j % WTN;
+        acc[a][b] = mfma32(fr[ks & 1][a], fr[ks & 1][WTM + b], acc[a][b]);
+        if constexpr (ks + 1 < NKS) {
+          // the W fragments first: every MFMA of a step uses one of them, the X fragments come in order of use
+          static_for<0, R>([&](auto pc) __attribute__((always_inline)) {
+            constexpr int pq = decltype(pc)::value;
+            constexpr int q = pq < WTN ? WTM + pq : pq - WTN;
+            if constexpr (pq * G / R == j) read(std::integral_constant<int, ks + 1>{}, std::integral_constant<int, q>{});
+          });
+        }
+        static_for<0, CPW>([&](auto cc) __attribute__((always_inline)) {
+          constexpr int c = decltype(cc)::value;
+          if constexpr ((c * NM) / CPW == i) cp(c);
+        });
+        __builtin_amdgcn_sched_barrier(0);
+      });
+    };
+#pragma unroll
+    for (int a = 0; a < WTM; ++a)
+#pragma unroll
+      for (int b = 0; b < WTN; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+
+    const int nk = (k1 - k0) / BK;
+    // prologue: slices 0 .. NS - 2 in flight; wait for slice 0
+#pragma unroll
+    for (int j = 0; j < NS - 1; ++j)
+      if (j < nk)
+#pragma unroll
+        for (int i = 0; i < CPW; ++i) copy_one(j, k0 + j * BK, i);
+    if (NS == 2 || nk == 1)
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(CPW));  // slice 1's copies may still be in flight
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      // slot (kt + NS - 1) % NS was last read in step kt - 1, before its closing barrier
+      const bool more = kt + NS - 1 < nk;
+      const int stn = (kt + NS - 1) % NS, kbn = k0 + (kt + NS - 1) * BK;
+      compute(kt % NS, [&](int i) __attribute__((always_inline)) {
+        if (more) copy_one(stn, kbn, i);
+      });
+      if (kt + 1 < nk) {
+        // slice kt + 1 must have landed; slice kt + 2 (NS = 3, if there is one: CPW copies) may still be in flight
+        if (NS == 3 && kt + 2 < nk)
+          __builtin_amdgcn_s_waitcnt(vmcnt_le(CPW));
+        else
+          __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+        __syncthreads();
+      }
+    }
+  }
+
   __device__ __forceinline__ static void mainloop(Lds& S, const uint16_t* __restrict__ x,
                                                   const uint16_t* __restrict__ w, long long ldx, int k0, int k1,
                                                   int M, int N, int m_blk, int n_blk, Acc& acc) {
+    // tiles with 5 or more MFMAs per 16-deep step take the fixed issue order; those with 4 (two 32-row by two
+    // 32-column blocks per wavefront) measured faster with the compiler's own order and all copies at the start
+    if constexpr (WTM * WTN >= 5) {
+      mainloop_pinned(S, x, w, ldx, k0, k1, M, N, m_blk, n_blk, acc);
+      return;
+    }
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm0 = wm(), wn0 = wn();
