@@ -723,16 +723,14 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
 
   const int P = gridDim.x;
   if constexpr (MODE == MODE_VARLEN) {
-    // packed sequences: the batched longest-first schedule of fmha_sched.h, computed alike by every workgroup
+    // packed sequences: the longest-first schedule of fmha_sched.h, computed alike by every workgroup
     vs_build<PP_BM>(vs, p.cu_seqlens, p.B, p.H, p.G, P, (int)blockIdx.x);
     if (vs.ok) {
       for (int r = 0; r < vs.rounds; ++r) {
-        const int k = vs.mine[r];
-        if (k < 0) continue;
-        int rank, head, level;
-        vs_decode(vs, p.H, (int)blockIdx.x % vs.nx, k, rank, head, level);
+        const int v = vs.mine[r];  // sequence * H + KV head, times 1024, plus row tile
+        if (v < 0) continue;
         exec_barrier();  // as below
-        item(vs.sorted[rank] * p.H + head, level);
+        item(v >> 10, v & 1023);
       }
       return;
     }

@@ -430,6 +430,19 @@ def test_varlen_full_tiles():
     FC.check_tolerance(og, o, lg, lse, where="varlen_full_tiles")
 
 
+# The item schedule's other shapes: 96 sequences with 4 KV heads (48 pairs per class of 32 workgroups, ~100 items
+# per class: six assignment rounds) and 300 sequences (beyond its 256-sequence tables: the fixed item order).
+@pytest.mark.parametrize("nseq,hi,Hkv,seed", [(96, 400, 4, 75), (300, 24, 2, 76)])
+def test_varlen_schedule_shapes(nseq, hi, Hkv, seed):
+    seqlens = [int(x) for x in np.random.default_rng(seed).integers(0, hi, size=nseq)]
+    c = FC.Case("varlen_sched", B=1, S=0, N=0, Hq=8, Hkv=Hkv, D=128, mode="varlen", seed=seed, seqlens=seqlens)
+    _say(f"varlen schedule shapes nseq {nseq} Hkv {Hkv} tokens {sum(seqlens)}")
+    a = FC.build(c)
+    og, lg = run_varlen(c, a)
+    o, lse = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, o, lg, lse, where=f"varlen_sched_{nseq}")
+
+
 def test_config3_varlen():
     cfg = W.CONFIGS[3]
     c = FC.Case(cfg.name, B=1, S=0, N=0, Hq=cfg.Hq, Hkv=cfg.Hkv, D=cfg.D, mode="varlen", seed=cfg.seed,
