@@ -142,7 +142,8 @@ struct DmaTile {
   static constexpr int CPW = (CH + NWAVES - 1) / NWAVES;   // chunks copied per wavefront per slice (at most)
   static constexpr bool EVEN = CPW * NWAVES == CH;         // otherwise the last wavefronts copy one fewer
   static_assert(NS == 2 || NS == 3, "two or three slices in the ring");
-  static_assert(EVEN || NS == 2, "the 3-slice ring's partial waits count whole chunks per wavefront");
+  static constexpr int CLAST = CH - (NWAVES - 1) * CPW;  // chunks of the last wavefront (CPW when EVEN)
+  static_assert(CLAST > 0 && CLAST <= CPW, "every wavefront copies at least one chunk");
 
   struct Lds {
     uint16_t xs[NS][BM * BK];
@@ -225,8 +226,10 @@ struct DmaTile {
         for (int i = 0; i < CPW; ++i) copy_one(j, k0 + j * BK, i);
     if (NS == 2 || nk == 1)
       __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
-    else
+    else if (EVEN || wv < NWAVES - 1)
       __builtin_amdgcn_s_waitcnt(vmcnt_le(CPW));  // slice 1's copies may still be in flight
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(CLAST));
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
       // slot (kt + NS - 1) % NS was last read in step kt - 1, before its closing barrier
@@ -236,11 +239,16 @@ struct DmaTile {
         if (more) copy_one(stn, kbn, i);
       });
       if (kt + 1 < nk) {
-        // slice kt + 1 must have landed; slice kt + 2 (NS = 3, if there is one: CPW copies) may still be in flight
-        if (NS == 3 && kt + 2 < nk)
-          __builtin_amdgcn_s_waitcnt(vmcnt_le(CPW));
-        else
+        // slice kt + 1 must have landed; slice kt + 2 (NS = 3, if there is one: this wavefront's copies of it) may
+        // still be in flight
+        if (NS == 3 && kt + 2 < nk) {
+          if (EVEN || wv < NWAVES - 1)
+            __builtin_amdgcn_s_waitcnt(vmcnt_le(CPW));
+          else
+            __builtin_amdgcn_s_waitcnt(vmcnt_le(CLAST));
+        } else {
           __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+        }
         __syncthreads();
       }
     }
@@ -305,19 +313,26 @@ struct DmaTile {
       if (j < nk) copy(j, k0 + j * BK);
     if (NS == 2 || nk == 1)
       __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
-    else
+    else if (EVEN || wv < NWAVES - 1)
       __builtin_amdgcn_s_waitcnt(vmcnt_le(CPW));  // slice 1's copies may still be in flight
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(CLAST));
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
       // slot (kt + NS - 1) % NS was last read in step kt - 1, before its closing barrier
       if (kt + NS - 1 < nk) copy((kt + NS - 1) % NS, k0 + (kt + NS - 1) * BK);
       compute(kt % NS);
       if (kt + 1 < nk) {
-        // slice kt + 1 must have landed; slice kt + 2 (NS = 3, if there is one: CPW copies) may still be in flight
-        if (NS == 3 && kt + 2 < nk)
-          __builtin_amdgcn_s_waitcnt(vmcnt_le(CPW));
-        else
+        // slice kt + 1 must have landed; slice kt + 2 (NS = 3, if there is one: this wavefront's copies of it) may
+        // still be in flight
+        if (NS == 3 && kt + 2 < nk) {
+          if (EVEN || wv < NWAVES - 1)
+            __builtin_amdgcn_s_waitcnt(vmcnt_le(CPW));
+          else
+            __builtin_amdgcn_s_waitcnt(vmcnt_le(CLAST));
+        } else {
           __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+        }
         __syncthreads();
       }
     }
@@ -332,7 +347,7 @@ using D128x128 = DmaTile<2, 2, 2, 2, 2>;      // 4 wavefronts, 64 KB
 using D256x128 = DmaTile<4, 2, 2, 2, 2>;      // 8 wavefronts of 64 x 64, 96 KB
 using D128x256 = DmaTile<2, 4, 2, 2, 2>;      // 8 wavefronts of 64 x 64, 96 KB
 using D256x256 = DmaTile<2, 4, 4, 2, 2>;      // 8 wavefronts of 128 x 64, 128 KB
-using D256x160 = DmaTile<8, 1, 1, 5, 2>;      // 8 wavefronts of 32 x 160, 104 KB (fills 256 CUs where N = 2560)
+using D256x160 = DmaTile<8, 1, 1, 5, 3>;      // 8 wavefronts of 32 x 160, 3 slices, 156 KB (fills 256 CUs at N = 2560)
 enum TileId : unsigned char { kT128x128 = 0, kD128x128 = 1, kD256x128 = 2, kD128x256 = 3, kD256x256 = 4, kD256x160 = 5 };
 constexpr const char* kTileNames[6] = {"mfma 128x128x64, 4 waves, register-staged", "mfma 128x128x64, 4 waves, LDS ring",
                                        "mfma 256x128x64, 8 waves, LDS ring", "mfma 128x256x64, 8 waves, LDS ring",
