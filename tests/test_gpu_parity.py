@@ -431,8 +431,9 @@ def test_varlen_full_tiles():
 
 
 # The item schedule's other shapes: 96 sequences with 4 KV heads (48 pairs per class of 32 workgroups, ~100 items
-# per class: six assignment rounds) and 300 sequences (beyond its 256-sequence tables: the fixed item order).
-@pytest.mark.parametrize("nseq,hi,Hkv,seed", [(96, 400, 4, 75), (300, 24, 2, 76)])
+# per class: six assignment rounds), 256 sequences with 8 KV heads (256 pairs per class: the pair table and its
+# prefix sums over all 64 lanes of the scan) and 300 sequences (beyond its 256-sequence tables: the fixed order).
+@pytest.mark.parametrize("nseq,hi,Hkv,seed", [(96, 400, 4, 75), (256, 200, 8, 77), (300, 24, 2, 76)])
 def test_varlen_schedule_shapes(nseq, hi, Hkv, seed):
     seqlens = [int(x) for x in np.random.default_rng(seed).integers(0, hi, size=nseq)]
     c = FC.Case("varlen_sched", B=1, S=0, N=0, Hq=8, Hkv=Hkv, D=128, mode="varlen", seed=seed, seqlens=seqlens)
