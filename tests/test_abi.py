@@ -56,6 +56,22 @@ def test_null_bias_returns_minus_one(loader):
     assert L.reax_fmha_b(*args) == -1  # v8:439: returns before any launch
 
 
+@pytest.mark.parametrize("loader", [abi.howu, abi.post])
+def test_fmha_empty_grid(loader):
+    # an empty query block or batch: hipErrorInvalidConfiguration (9), the code of the reference's own launch with a
+    # zero-sized grid; returned before any HIP call (the buffers are never touched, so aligned stand-in addresses do)
+    L = loader()
+    q, k, v, qpos, o = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+    strides = [8 * 256, 256, 256] * 4  # qs/ks/vs/os B, H, M: multiples of 8 elements
+    q_args = lambda B, M: [q, k, v, qpos, 1, 0, o, ctypes.c_float(0.0625), B, 1, M, 16] + strides + [None]
+    assert L.reax_fmha_q(*q_args(1, 0)) == 9
+    assert L.reax_fmha_q(*q_args(0, 64)) == 9
+    if loader is abi.howu:
+        x_args = lambda M, D: [q, k, v, qpos, 1, 0, o, None, ctypes.c_float(0.0625), 1, 1, M, 16, D] + [8 * D] * 18 + [None]
+        assert L.reax_fmha_qx(*x_args(0, 128)) == 9
+        assert L.reax_fmha_qx(*x_args(0, 256)) == 9
+
+
 def test_rarn_argument_codes():
     # reax_rarn (rarn_final.cu:100, 104): n <= 0 -> 0 (even with a wrong D), D != 2560 -> -1, S outside 2..8 -> -2;
     # a missing buffer (which the reference would fault on) -> hipErrorInvalidValue; none of these launches
