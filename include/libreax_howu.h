@@ -55,7 +55,9 @@ int reax_fmha_qx(const void* q, const void* k, const void* v, const int* qpos, i
  * Q/O [T][Hq][D] and K/V [T][Hkv][D] (token strides qsT/ksT/vsT/osT, head strides qsH/ksH/vsH/osH); token i of
  * a sequence sees that sequence's tokens 0..i only. cu_seqlens (int32, nseq+1 entries, device memory) starts at
  * 0 and is non-decreasing; max_seqlen >= every sequence length. lse (optional) is [T][Hq] with strides
- * lsT/lsH. Hq must be a multiple of Hkv. */
+ * lsT/lsH. Hq must be a multiple of Hkv. max_seqlen sizes the launch and cu_seqlens is device memory the host
+ * does not read, so a max_seqlen below some sequence's length is not detected: that sequence's tokens past
+ * max_seqlen may be left unwritten in o and lse (flash-attention's varlen interface has the same precondition). */
 int reax_fmha_varlen(const void* q, const void* k, const void* v, const int* cu_seqlens, int nseq, int max_seqlen,
                      void* o, float* lse, float scale, int Hq, int Hkv, int D, long long qsT, long long qsH,
                      long long ksT, long long ksH, long long vsT, long long vsH, long long osT, long long osH,

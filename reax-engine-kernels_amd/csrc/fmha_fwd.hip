@@ -1082,11 +1082,12 @@ int launch_fwd(const FwdParams& p0, int head_dim, int mode, bool post, hipStream
   // ping-pong kernel once there are rows for both of its groups (fmha_fwd_pair.hip)
   if (head_dim == 256 && (mode == MODE_QPOS || (mode == MODE_VARLEN && !post)) && p.M > 64)
     return launch_fwd_pair(p, mode, post, stream);
+  // head_dim 128 is reached only through the extension entry points (qpos or varlen, no gate, no bias); the
+  // drop-in entry points (bias, POST, block rule) run at head_dim 256
   if (head_dim == 128) {
-    if (mode == MODE_QPOS)
-      return post ? launch_fwd_t<128, MODE_QPOS, true, false>(p, stream) : launch_fwd_t<128, MODE_QPOS, false, false>(p, stream);
-    if (mode == MODE_BIAS && !post) return launch_fwd_t<128, MODE_BIAS, false, false>(p, stream);
-    if (mode == MODE_VARLEN && !post) return launch_fwd_t<128, MODE_VARLEN, false, false>(p, stream);
+    if (post || p.qpos0_block) return (int)hipErrorInvalidValue;
+    if (mode == MODE_QPOS) return launch_fwd_t<128, MODE_QPOS, false, false>(p, stream);
+    if (mode == MODE_VARLEN) return launch_fwd_t<128, MODE_VARLEN, false, false>(p, stream);
   } else if (head_dim == 256) {
     if (mode == MODE_QPOS)
       return post ? launch_fwd_t<256, MODE_QPOS, true, false>(p, stream) : launch_fwd_t<256, MODE_QPOS, false, false>(p, stream);

@@ -390,10 +390,13 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pair_kernel(const FwdParams p
 }
 
 template <int MODE, bool POST>
-static int launch_t(FwdParams p, int cus, hipStream_t stream) {
+static int launch_t(FwdParams p, hipStream_t stream) {
   p.n_tiles = (int)(((long long)p.M + PR_BM - 1) / PR_BM);
   const long long n_items = (long long)p.B * p.H * p.n_tiles;
+  // an empty grid is rejected before any HIP call, as the reference's zero-sized launch would fail
   if (n_items <= 0 || n_items > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  const int cus = device_cus(stream);
+  if (cus <= 0) return (int)hipErrorInvalidDevice;
   const long long nwg = n_items < cus ? n_items : cus;  // one workgroup per CU (its LDS and registers fill one)
   const int o_vec8 = (!POST && p.o) ? (aligned_elems(p.o, 4, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0) : 0;
   hipLaunchKernelGGL((fmha_fwd_pair_kernel<MODE, POST>), dim3((unsigned)nwg), dim3(64 * PR_NW), 0, stream, p, o_vec8);
@@ -401,10 +404,8 @@ static int launch_t(FwdParams p, int cus, hipStream_t stream) {
 }
 
 int launch_fwd_pair(const FwdParams& p, int mode, bool post, hipStream_t stream) {
-  const int cus = device_cus(stream);
-  if (cus <= 0) return (int)hipErrorInvalidDevice;
-  if (mode == MODE_QPOS) return post ? launch_t<MODE_QPOS, true>(p, cus, stream) : launch_t<MODE_QPOS, false>(p, cus, stream);
-  if (mode == MODE_VARLEN && !post) return launch_t<MODE_VARLEN, false>(p, cus, stream);
+  if (mode == MODE_QPOS) return post ? launch_t<MODE_QPOS, true>(p, stream) : launch_t<MODE_QPOS, false>(p, stream);
+  if (mode == MODE_VARLEN && !post) return launch_t<MODE_VARLEN, false>(p, stream);
   return (int)hipErrorInvalidValue;
 }
 

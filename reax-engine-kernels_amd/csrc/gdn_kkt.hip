@@ -269,7 +269,7 @@ extern "C" int reax_kkt(const void* k, const void* g, const void* beta, void* A,
       (reinterpret_cast<uintptr_t>(A) & 3u) || (reinterpret_cast<uintptr_t>(cu) & 7u) ||
       (reinterpret_cast<uintptr_t>(cidx) & 7u))
     return (int)hipErrorInvalidValue;
-  // persistent grid: four workgroups per compute unit (the LDS and register budget), at most one per item
+  // persistent grid: KKT_WG_PER_CU workgroups per compute unit (the LDS and register budget), at most one per item
   const long long items = (long long)NT * H;
   if (items > INT32_MAX) return (int)hipErrorInvalidConfiguration;
   const int cus = device_cus(static_cast<hipStream_t>(stream));

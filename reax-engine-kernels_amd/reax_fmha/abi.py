@@ -13,8 +13,8 @@ import ctypes
 import os
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-# REAX_FMHA_LIB_DIR selects another build of the two libraries (e.g. a tuning variant); default: in-tree lib/
-LIB_DIR = os.environ.get("REAX_FMHA_LIB_DIR") or os.path.join(PKG_ROOT, "lib")
+# always the in-tree build: no environment variable redirects the product loader to another build
+LIB_DIR = os.path.join(PKG_ROOT, "lib")
 HOWU_PATH = os.path.join(LIB_DIR, "libreax_howu.so")
 POST_PATH = os.path.join(LIB_DIR, "libreax_fmha_post.so")
 

@@ -66,10 +66,13 @@ def test_fmha_empty_grid(loader):
     q_args = lambda B, M: [q, k, v, qpos, 1, 0, o, ctypes.c_float(0.0625), B, 1, M, 16] + strides + [None]
     assert L.reax_fmha_q(*q_args(1, 0)) == 9
     assert L.reax_fmha_q(*q_args(0, 64)) == 9
+    assert L.reax_fmha_q(*q_args(0, 200)) == 9  # more than 64 rows: the wavefront-pair kernel's launcher
     if loader is abi.howu:
-        x_args = lambda M, D: [q, k, v, qpos, 1, 0, o, None, ctypes.c_float(0.0625), 1, 1, M, 16, D] + [8 * D] * 18 + [None]
-        assert L.reax_fmha_qx(*x_args(0, 128)) == 9
-        assert L.reax_fmha_qx(*x_args(0, 256)) == 9
+        x_args = lambda B, M, D: [q, k, v, qpos, 1, 0, o, None, ctypes.c_float(0.0625), B, 1, M, 16, D] + [8 * D] * 18 + [None]
+        assert L.reax_fmha_qx(*x_args(1, 0, 128)) == 9
+        assert L.reax_fmha_qx(*x_args(1, 0, 256)) == 9
+        assert L.reax_fmha_qx(*x_args(0, 300, 128)) == 9  # the persistent head_dim-128 kernel's launcher
+        assert L.reax_fmha_qx(*x_args(0, 300, 256)) == 9
 
 
 def test_rarn_argument_codes():

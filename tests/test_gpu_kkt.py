@@ -30,8 +30,10 @@ def _dev(a):
 
 
 @pytest.mark.parametrize("lens,H,seed", [([64], 1, 10), ([130, 64, 45], 2, 11), ([1, 2, 63, 65, 200], 4, 12),
-                                          ([512, 300], 8, 13)])
+                                          ([512, 300], 8, 13), ([4096, 4000, 130], 8, 15)])
 def test_kkt_matches_oracle(lens, H, seed):
+    # the last case has 130 chunks x 8 key heads = 1040 items, more than the persistent grid's KKT_WG_PER_CU (3)
+    # workgroups on each of 256 CUs: workgroups run a second item (the prefetched next item, LDS reused)
     from reax_fmha import ops
 
     a = KC.make_inputs(lens, H, seed)
