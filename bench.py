@@ -186,6 +186,48 @@ def bench_decode(torch, ops, iters, num_splits=None):
     return cfg, ms, gbs
 
 
+def bench_qp_decode(torch, ops, cfg, iters):
+    """The drop-in decode call: reax_fmha_qp (libreax_fmha_post.so) on one query token per sequence, Q folded
+    [B][Hkv][G][256], K/V caches [B][N][Hkv][256] (every key visible), qg [B][Hq][512] with the gate in the second
+    half, out [B][Hq*256], inv = b. Median over `iters` launches, each after a 512 MB write that evicts L2/MALL."""
+    q, k, v, qpos = W.make_decode_inputs(cfg)
+    gate = W.make_gate(cfg)
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, D, G = cfg.B, cfg.Hq, cfg.Hkv, cfg.D, cfg.G
+    qd = W.bits_to_torch(np.ascontiguousarray(q.reshape(B, 1, Hkv, G, D).transpose(0, 2, 1, 3, 4)
+                                              .reshape(B, Hkv, G, D)), dev)
+    kd, vd = W.bits_to_torch(k, dev), W.bits_to_torch(v, dev)
+    del k, v
+    qg = torch.empty((B, Hq, 2 * D), dtype=torch.bfloat16, device=dev)
+    qg[:, :, :D] = W.bits_to_torch(q.reshape(B, Hq, D), dev)
+    qg[:, :, D:] = W.bits_to_torch(gate.reshape(B, Hq, D), dev)
+    out = torch.empty((B, Hq * D), dtype=torch.bfloat16, device=dev)
+    inv = torch.arange(B, dtype=torch.int32, device=dev).reshape(B, 1)
+    qp = torch.from_numpy(qpos).to(dev)
+    scale = float(np.float32(cfg.scale))
+    run = lambda: ops.fmha_qp(qd, kd, vd, qp, G, scale, inv, 1, qg, out)
+    fl = flush_buffer(torch)
+    for _ in range(3):
+        run()
+    times = []
+    for _ in range(iters):
+        fl.fill_(1)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        run()
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+    del fl
+    ms = float(np.median(times))
+    gbs = cfg.decode_bytes() / (ms * 1e-3) / 1e9
+    return {"workload": cfg.name, "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
+            "bytes": cfg.decode_bytes(), "B": B, "N": cfg.N, "Hq": Hq, "Hkv": Hkv, "D": D, "Lq": 1,
+            "entry_point": "reax_fmha_qp (libreax_fmha_post.so): drop-in ABI, sigmoid gate epilogue",
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / W.HBM_PEAK_GBS, 4), "traffic": None}}
+
+
 # ----------------------------------------------------------------------------------------- CPU baseline
 
 
@@ -517,7 +559,7 @@ def bench_gemm(torch, ops, iters=20):
 
 
 PROFILES = os.path.join(ROOT, "profiles")
-LEGS = ["prefill", "c1", "c3", "c5", "decode", "rarn", "conv", "kkt", "howu", "gemm"]
+LEGS = ["prefill", "c1", "c3", "c5", "decode", "qp_decode", "rarn", "conv", "kkt", "howu", "gemm"]
 
 
 def main():
@@ -592,6 +634,10 @@ def main():
         print(json.dumps({"rarn_GBs": round(gbs, 1), "ms": round(ms, 4), "rows": RARN_N, "partials": RARN_S}),
               flush=True)
         return
+    if one == "qp_decode":
+        for B, qcfg in W.DROPIN_DECODE.items():
+            print(json.dumps(bench_qp_decode(torch, ops, qcfg, args.iters)), flush=True)
+        return
     if one == "decode":
         dcfg, dms, gbs = bench_decode(torch, ops, args.steps, args.decode_splits)
         print(json.dumps({"decode_GBs": round(gbs, 1), "ms": round(dms, 4), "splits": dcfg.num_splits}), flush=True)
@@ -631,6 +677,9 @@ def main():
                           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": W.HBM_PEAK_GBS,
                                        "unit": "GB/s", "frac": round(gbs / W.HBM_PEAK_GBS, 4),
                                        "traffic": pmc_traffic(os.path.join(PROFILES, "fmha_decode_c4_pmc.txt"))}}
+        for B, qcfg in W.DROPIN_DECODE.items():
+            legs[f"qp_decode_b{B}"] = bench_qp_decode(torch, ops, qcfg, 20)
+            torch.cuda.empty_cache()
     if not args.no_configs:
         for name in ("c1", "c3", "c5"):
             mk, ccfg, entry = preps[name]

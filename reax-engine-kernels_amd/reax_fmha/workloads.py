@@ -50,6 +50,9 @@ class Config:
 
     def decode_bytes(self) -> int:
         kv = 2 * self.B * self.N * self.Hkv * self.D * 2
+        if self.kind == "decode_post":
+            # the drop-in reax_fmha_qp: Q read, the gate half of qg read, the gated output written; no LSE
+            return kv + 3 * self.B * self.S * self.Hq * self.D * 2
         qo = 2 * self.B * self.S * self.Hq * self.D * 2
         return kv + qo + self.B * self.S * self.Hq * 4
 
@@ -67,6 +70,15 @@ CONFIGS = {
     4: Config("c4_decode_splitkv_kv8192_d128", "decode", B=16, S=1, N=8192, Hq=32, Hkv=8, D=128, seed=1004,
               num_splits=16),
     5: Config("c5_causal_gqa_s32768_d256_gated", "post", B=1, S=32768, N=32768, Hq=16, Hkv=2, D=256, seed=1005),
+}
+
+# The engine's per-token decode call through the drop-in reax_fmha_qp (config 5's model: Hq 16, Hkv 2, D 256, the
+# sigmoid gate): one query token per sequence (Lq 1 x G 8 = 8 folded rows per KV head) over a 32768-key cache, at
+# batch 1 and 16. Memory-bound: reported in HBM GB/s of K + V + Q + gate + output.
+DROPIN_DECODE = {
+    B: Config(f"qp_decode_b{B}_kv32768_d256_gated", "decode_post", B=B, S=1, N=32768, Hq=16, Hkv=2, D=256,
+              seed=1006 + B)
+    for B in (1, 16)
 }
 
 
