@@ -763,23 +763,42 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// Split-KV decode for short query blocks (head_dim 128, at most 32 folded rows per (b, KV head)). The key range of
-// each (b, KV head) is cut into num_splits splits of split_len keys; each split is streamed by P = 1, 2 or 4
-// wavefronts (p.wpsplit), each over its own part of split_len / P keys (a whole number of 64-key tiles) through a
-// private LDS region (a K and a V tile), so the loop has no workgroup barrier: the next K tile loads while the
-// softmax and P.V of the current tile run, the next V tile while the next S^T runs. All G query heads of the KV
-// head share each K/V tile. A workgroup's 4 wavefronts take 4 / P consecutive (b, split, KV head) tasks, KV head
-// fastest, so with P = 1 they read neighbouring 256-byte head slices of the same cache rows together. At the end
-// the P partials of a split merge through LDS into the split's partial (O / l in fp32 and its natural-log LSE),
-// which splitkv_combine_kernel merges across splits.
+// Split-KV decode for short query blocks (at most 32 folded rows per (b, KV head)). The key range of each (b, KV
+// head) is cut into num_splits splits of split_len keys; each split is streamed by P = 1, 2 or 4 wavefronts
+// (p.wpsplit), each over its own part of split_len / P keys (a whole number of key tiles) through a private LDS
+// region (a K and a V tile), so the loop has no workgroup barrier: the next K tile loads while the softmax and P.V
+// of the current tile run, the next V tile while the next S^T runs. All G query heads of the KV head share each
+// K/V tile. A workgroup's 4 wavefronts take 4 / P consecutive (b, split, KV head) tasks, KV head fastest, so with
+// P = 1 they read neighbouring head slices of the same cache rows together. At the end the P partials of a split
+// merge through LDS into the split's partial (O / l in fp32 and its natural-log LSE), which
+// splitkv_combine_kernel merges across splits.
+// A tile is 16 KB at either head dim: 64 keys at head_dim 128, 32 keys at head_dim 256.
+// BLK0: the drop-in entry points' block rule (all rows of (b, h) form one block of at most 32 rows: when the
+// largest raw qpos among them is 0, every live row sees key 0 only, reax_fmha_v8.cu:155-162, 224-235).
 constexpr int DEC_NW = 4;
 
 template <int HD>
+struct DecTile {
+  static constexpr int BN = HD == 128 ? 64 : 32;  // keys per tile
+  static constexpr int NKB = BN / 32;             // 32-key blocks of S^T per tile
+  static constexpr int NSS = BN / 16;             // 16-key MFMA steps of P.V per tile
+  static constexpr int TILE = BN * HD * 2;        // 16 KB
+  static constexpr int QK = HD / 16, DB = HD / 32;
+  static_assert(TILE == 16384, "two 16 KB tiles per wavefront, four wavefronts: 128 KB of LDS");
+};
+
+template <int HD, bool BLK0>
 __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, int wpsplit) {
-  using T = FwdTile<HD>;
-  static_assert(HD == 128, "the decode kernel keeps 2 x 16 KB of LDS per wavefront");
-  __shared__ __align__(1024) uint8_t kbuf[DEC_NW][T::TILE];
-  __shared__ __align__(1024) uint8_t vbuf[DEC_NW][T::TILE];
+  using T = DecTile<HD>;
+  // the K and V tiles of the four wavefronts; after the key loop the same bytes hold the partials being merged
+  // (DEC_NW x 32 rows x HD fp32: 64 KB at head_dim 128, all 128 KB at 256)
+  struct Lds {
+    uint8_t k[DEC_NW][T::TILE];
+    uint8_t v[DEC_NW][T::TILE];
+  };
+  static_assert(sizeof(Lds) >= DEC_NW * 32 * HD * sizeof(float), "merge area");
+  __shared__ __align__(1024) Lds L;
+  __shared__ float mm[DEC_NW * 32], lm[DEC_NW * 32];
   const int tid = threadIdx.x, lane = tid & 63, hf = lane >> 5, lr = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wavefront-uniform: keeps the loop control scalar
   const int P = wpsplit, part = w % P;
@@ -797,8 +816,10 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   const int r = lr;  // row (folded: token r/G, head r%G); p.M <= 32
   const bool rvalid = r < p.M;
   const int tok = rvalid ? r / p.G : 0, g = rvalid ? r - tok * p.G : 0;
-  int lim = -1;
-  if (rvalid && active) lim = max(min(p.qpos[(long long)b * p.qpBs + tok], wend - 1), -1);
+  int qr = -1;
+  if (rvalid && active) qr = p.qpos[(long long)b * p.qpBs + tok];
+  if (BLK0 && p.N > 0 && wave_max(qr) == 0 && rvalid) qr = 0;  // the block rule: every live row sees key 0
+  int lim = max(min(qr, wend - 1), -1);
   if (lim < wbeg) lim = -1;
   const int wmax = __builtin_amdgcn_readfirstlane(wave_max(lim));
   const int wmin = __builtin_amdgcn_readfirstlane(wave_min(lim));
@@ -812,13 +833,15 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   __builtin_amdgcn_s_waitcnt(vmcnt_le(0));  // Q has landed before the (untracked) tile loads start
   const uint16_t* Kb = p.k + (long long)b * p.ksB + (long long)hk * p.ksH;
   const uint16_t* Vb = p.v + (long long)b * p.vsB + (long long)hk * p.vsH;
-  const Dma<HD, 1> kplan(p.ksM, 0, lane), vplan(p.vsM, 0, lane);
+  const Dma<HD, 1, T::BN> kplan(p.ksM, 0, lane), vplan(p.vsM, 0, lane);
   const bool kfast = p.ksM * 2 * T::BN < (1ll << 31), vfast = p.vsM * 2 * T::BN < (1ll << 31);
-  const uint32_t kbase[2] = {k_lane_base<HD>(0, lr, hf), k_lane_base<HD>(1, lr, hf)};
+  uint32_t kbase[T::NKB];
+#pragma unroll
+  for (int kb = 0; kb < T::NKB; ++kb) kbase[kb] = k_lane_base<HD>(kb, lr, hf);
   const uint32_t vbase = v_lane_base<HD>(lane);
-  constexpr int DW = Dma<HD, 1>::DW;
-  uint8_t* kb = kbuf[w];
-  uint8_t* vb = vbuf[w];
+  constexpr int DW = Dma<HD, 1, T::BN>::DW;
+  uint8_t* kb_ = L.k[w];
+  uint8_t* vb_ = L.v[w];
 
   f32x16_t o[T::DB];
 #pragma unroll
@@ -827,34 +850,43 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
     for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
   const float cc = p.scale_log2;
-  f32x16_t s[2];
-  uint32_t pk[2][8];
+  f32x16_t s[T::NKB];
+  uint32_t pk[T::NKB][8];
 
   if (t_end > t_beg) {
-    kplan.template tile<2>(kb, Kb, p.ksM, kfast, t_beg * T::BN, wend, 0, lane);
-    vplan.template tile<2>(vb, Vb, p.vsM, vfast, t_beg * T::BN, wend, 0, lane);
+    kplan.template tile<2>(kb_, Kb, p.ksM, kfast, t_beg * T::BN, wend, 0, lane);
+    vplan.template tile<2>(vb_, Vb, p.vsM, vfast, t_beg * T::BN, wend, 0, lane);
   }
   for (int t = t_beg; t < t_end; ++t) {
     const int k0 = t * T::BN;
     const bool more = t + 1 < t_end;
     __builtin_amdgcn_s_waitcnt(vmcnt_le(DW));  // K(t) landed (V(t) may be in flight)
-    qk_tile<HD>(s, kb, qf, kbase);
+#pragma unroll
+    for (int kb = 0; kb < T::NKB; ++kb) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[kb][e] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < T::QK; ++ks) {
+        const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb_ + (kbase[kb] ^ (32u * ks)));
+        s[kb] = mfma32(as_bf16x8(kf), qf[ks], s[kb]);
+      }
+    }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the K tile has been read
-    if (more) kplan.template tile<2>(kb, Kb, p.ksM, kfast, k0 + T::BN, wend, 0, lane);
+    if (more) kplan.template tile<2>(kb_, Kb, p.ksM, kfast, k0 + T::BN, wend, 0, lane);
     if (k0 + T::BN - 1 > wmin) {
 #pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2)
+      for (int kb = 0; kb < T::NKB; ++kb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int key = k0 + 32 * kb2 + 8 * (v >> 2) + 4 * hf + (v & 3);
-          if (key > lim) s[kb2][v] = -INFINITY;
+          const int key = k0 + 32 * kb + 8 * (v >> 2) + 4 * hf + (v & 3);
+          if (key > lim) s[kb][v] = -INFINITY;
         }
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2)
+    for (int kb = 0; kb < T::NKB; ++kb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb2][v]);
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
     mx = halves_max(mx) * cc;
     if (__any(mx > m_run + RESCALE_SLACK)) {
       const float m_new = fmaxf(m_run, mx);
@@ -869,14 +901,14 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float ps[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; ++kb2)
+    for (int kb = 0; kb < T::NKB; ++kb)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float p0 = fast_exp2(__builtin_fmaf(s[kb2][2 * i], cc, -m_use));
-        const float p1 = fast_exp2(__builtin_fmaf(s[kb2][2 * i + 1], cc, -m_use));
+        const float p0 = fast_exp2(__builtin_fmaf(s[kb][2 * i], cc, -m_use));
+        const float p1 = fast_exp2(__builtin_fmaf(s[kb][2 * i + 1], cc, -m_use));
         ps[(i & 1) * 2] += p0;
         ps[(i & 1) * 2 + 1] += p1;
-        pk[kb2][i] = pack_bf16x2(p0, p1);
+        pk[kb][i] = pack_bf16x2(p0, p1);
       }
     l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
     if (more)
@@ -884,24 +916,22 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
     else
       __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
 #pragma unroll
-    for (int ss = 0; ss < 4; ++ss) {
+    for (int ss = 0; ss < T::NSS; ++ss) {
       const u32x4_t pw = {pk[ss >> 1][4 * (ss & 1) + 0], pk[ss >> 1][4 * (ss & 1) + 1], pk[ss >> 1][4 * (ss & 1) + 2],
                           pk[ss >> 1][4 * (ss & 1) + 3]};
       const bf16x8_t pb = as_bf16x8(pw);
 #pragma unroll
-      for (int db = 0; db < T::DB; ++db) o[db] = mfma32(v_operand<HD>(vb, db, ss, vbase), pb, o[db]);
+      for (int db = 0; db < T::DB; ++db) o[db] = mfma32(v_operand<HD>(vb_, db, ss, vbase), pb, o[db]);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the V tile has been read
-    if (more) vplan.template tile<2>(vb, Vb, p.vsM, vfast, k0 + T::BN, wend, 0, lane);
+    if (more) vplan.template tile<2>(vb_, Vb, p.vsM, vfast, k0 + T::BN, wend, 0, lane);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
 
   // ---- merge the P partials of each split through LDS (the tile buffers are free once every wavefront is here)
   const float l = halves_sum(l_run);
   __syncthreads();
-  float* om = reinterpret_cast<float*>(&kbuf[0][0]);  // [DEC_NW][32 rows][HD]: wavefront w's slice is kbuf[w]
-  float* mm = reinterpret_cast<float*>(&vbuf[0][0]);  // [DEC_NW][32]
-  float* lm = mm + DEC_NW * 32;                       // [DEC_NW][32]
+  float* om = reinterpret_cast<float*>(&L);  // [DEC_NW][32 rows][HD]
 #pragma unroll
   for (int db = 0; db < T::DB; ++db)
 #pragma unroll
@@ -951,10 +981,13 @@ __device__ __forceinline__ float wave_sumf(float x) {
   return x;
 }
 
-template <int HD>
+// POST: the drop-in reax_fmha_qp's epilogue instead of the O / LSE store (reax_fmha_v11.cu:451-522): O rounded to
+// bf16, times the bf16 sigmoid of the gate qg[R][hq][HD + d], rounded once, stored to out[R][hq * HD + d] for the
+// token row R = inv[b * Lq + token]; rows with R < 0 are left untouched.
+template <int HD, bool POST>
 __global__ void __launch_bounds__(256) splitkv_combine_kernel(const FwdParams p) {
   constexpr int DPL = HD / 64;  // dims per lane
-  constexpr int BATCH = 8;
+  constexpr int BATCH = 16;
   const long long wid = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (wid >= (long long)p.B * p.H * p.M) return;
@@ -997,6 +1030,21 @@ __global__ void __launch_bounds__(256) splitkv_combine_kernel(const FwdParams p)
   }
   const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
   const int tok = r / p.G, g = r - tok * p.G;
+  if (POST) {
+    const int R = p.inv[(long long)b * p.Lq + tok];
+    if (R < 0) return;
+    const long long hq = (long long)hk * p.G + g;
+    const uint16_t* grow = p.qg + (long long)R * p.qg_rs + hq * (2 * HD) + HD + DPL * lane;
+    uint16_t* orow = p.outp + (long long)R * p.out_rs + hq * HD + DPL * lane;
+#pragma unroll
+    for (int j = 0; j < DPL; j += 2) {
+      const uint32_t gw = *reinterpret_cast<const uint32_t*>(grow + j);
+      const uint32_t ob = pack_bf16x2(acc[j] * inv, acc[j + 1] * inv);
+      const uint32_t s0 = sigmoid_bf16_bits(gw & 0xffffu), s1 = sigmoid_bf16_bits(gw >> 16);
+      *reinterpret_cast<uint32_t*>(orow + j) = pack_bf16x2(bf16lo(ob) * bf16lo(s0), bf16hi(ob) * bf16lo(s1));
+    }
+    return;
+  }
   if (p.lse && lane == 0)
     p.lse[(long long)b * p.lsB + (long long)hk * p.lsH + (long long)tok * p.lsT + (long long)g * p.lsG] =
         wsum > 0.f ? mx + logf(wsum) : -INFINITY;
@@ -1078,6 +1126,11 @@ int launch_fwd(const FwdParams& p0, int head_dim, int mode, bool post, hipStream
     if (mode == MODE_QPOS) return launch_fwd_pp<MODE_QPOS>(p, stream);
     if (mode == MODE_VARLEN) return launch_fwd_pp<MODE_VARLEN>(p, stream);
   }
+  // the drop-in entry points at short query blocks (decode steps): key splits across the GPU when worthwhile
+  if (head_dim == 256 && mode == MODE_QPOS && p.qpos0_block && p.M <= 32) {
+    const int rc = launch_short_split(p, post, stream);
+    if (rc != SHORT_NOT_TAKEN) return rc;
+  }
   // head_dim 256 qpos / varlen (the drop-in shape, with or without the POST epilogue): the wavefront-pair
   // ping-pong kernel once there are rows for both of its groups (fmha_fwd_pair.hip)
   if (head_dim == 256 && (mode == MODE_QPOS || (mode == MODE_VARLEN && !post)) && p.M > 64)
@@ -1105,6 +1158,48 @@ size_t splitkv_workspace_bytes(int B, int H, int M, int head_dim, int num_splits
   return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
 }
 
+// Key-split parameters of the decode kernel for num_splits requested splits over N keys: P wavefronts per split
+// (each streaming at least DEC_MIN_TILES tiles when the split is long enough) and split_len, a multiple of P tiles.
+static void decode_split_shape(int head_dim, int N, int num_splits, int& P, int& split_len) {
+  constexpr int DEC_MIN_TILES = 8;
+  const int BN = head_dim == 128 ? DecTile<128>::BN : DecTile<256>::BN;
+  const int q = (N + num_splits - 1) / num_splits;
+  const int qt = max(1, (q + BN - 1) / BN);
+  P = qt >= 4 * DEC_MIN_TILES ? 4 : qt >= 2 * DEC_MIN_TILES ? 2 : 1;
+  split_len = ((qt + P - 1) / P) * P * BN;
+}
+
+int launch_decode_split(FwdParams p, int head_dim, int P, bool post, hipStream_t stream) {
+  const long long ntask = (long long)p.B * p.H * p.num_splits;
+  const long long nwg = (ntask + (DEC_NW / P) - 1) / (DEC_NW / P);
+  if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  const long long nrow = (long long)p.B * p.H * p.M;
+  const long long cwg = (nrow + 3) / 4;
+  if (cwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  if (head_dim == 128) {
+    if (post || p.qpos0_block) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL((fmha_decode_kernel<128, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
+  } else if (p.qpos0_block) {
+    hipLaunchKernelGGL((fmha_decode_kernel<256, true>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
+  } else {
+    hipLaunchKernelGGL((fmha_decode_kernel<256, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
+  }
+  if (const int rc = (int)hipGetLastError()) return rc;
+  if (head_dim == 128)
+    hipLaunchKernelGGL((splitkv_combine_kernel<128, false>), dim3((unsigned)cwg), dim3(256), 0, stream, p);
+  else if (post)
+    hipLaunchKernelGGL((splitkv_combine_kernel<256, true>), dim3((unsigned)cwg), dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((splitkv_combine_kernel<256, false>), dim3((unsigned)cwg), dim3(256), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
+void set_workspace(FwdParams& p, void* ws, int head_dim) {
+  const size_t rows = (size_t)p.B * p.H * p.num_splits * p.M;
+  p.ws_o = reinterpret_cast<float*>(ws);
+  p.ws_lse = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(ws) + align256(rows * head_dim * sizeof(float)));
+}
+
 int launch_splitkv(const SplitParams& sp, int head_dim, hipStream_t stream) {
   FwdParams p = sp.f;
   if (const int rc = prepare(p, false)) return rc;
@@ -1112,40 +1207,28 @@ int launch_splitkv(const SplitParams& sp, int head_dim, hipStream_t stream) {
   if (!aligned_elems(p.o, 2, {p.osB, p.osH, p.osT, p.osG})) return (int)hipErrorInvalidValue;
   const size_t need = splitkv_workspace_bytes(p.B, p.H, p.M, head_dim, sp.num_splits);
   if (need == 0 || sp.ws_bytes < need || (reinterpret_cast<uintptr_t>(sp.ws) & 255u)) return (int)hipErrorInvalidValue;
-  const size_t rows = (size_t)p.B * p.H * sp.num_splits * p.M;
-  p.ws_o = reinterpret_cast<float*>(sp.ws);
-  p.ws_lse = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(sp.ws) + align256(rows * head_dim * sizeof(float)));
   p.num_splits = sp.num_splits;
+  set_workspace(p, sp.ws, head_dim);
+  if ((head_dim == 128 || head_dim == 256) && p.M <= 32) {
+    // wavefront-split decode kernel: P wavefronts per split
+    int P;
+    decode_split_shape(head_dim, p.N, sp.num_splits, P, p.split_len);
+    return launch_decode_split(p, head_dim, P, false, stream);
+  }
   const int per = (p.N + sp.num_splits - 1) / sp.num_splits;
   p.split_len = ((per + FwdTile<128>::BN - 1) / FwdTile<128>::BN) * FwdTile<128>::BN;
   if (p.split_len <= 0) p.split_len = FwdTile<128>::BN;
-  int rc;
-  if (head_dim == 128 && p.M <= 32) {
-    // wavefront-split decode kernel: P wavefronts per split, each streaming at least DEC_MIN_TILES tiles when the
-    // split is long enough; split_len is a multiple of P tiles
-    constexpr int BN = FwdTile<128>::BN, DEC_MIN_TILES = 8;
-    const int q = (p.N + sp.num_splits - 1) / sp.num_splits;
-    const int qt = (q + BN - 1) / BN;
-    const int P = qt >= 4 * DEC_MIN_TILES ? 4 : qt >= 2 * DEC_MIN_TILES ? 2 : 1;
-    p.split_len = ((qt + P - 1) / P) * P * BN;
-    const long long ntask = (long long)p.B * p.H * p.num_splits;
-    const long long nwg = (ntask + (DEC_NW / P) - 1) / (DEC_NW / P);
-    if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
-    hipLaunchKernelGGL(fmha_decode_kernel<128>, dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
-    rc = (int)hipGetLastError();
-  } else {
-    rc = head_dim == 128 ? launch_fwd_t<128, MODE_QPOS, false, true>(p, stream)
-       : head_dim == 256 ? launch_fwd_t<256, MODE_QPOS, false, true>(p, stream)
-                         : (int)hipErrorInvalidValue;
-  }
+  int rc = head_dim == 128 ? launch_fwd_t<128, MODE_QPOS, false, true>(p, stream)
+         : head_dim == 256 ? launch_fwd_t<256, MODE_QPOS, false, true>(p, stream)
+                           : (int)hipErrorInvalidValue;
   if (rc) return rc;
   const long long nrow = (long long)p.B * p.H * p.M;
   const long long nwg = (nrow + 3) / 4;
   if (nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
   if (head_dim == 128)
-    hipLaunchKernelGGL(splitkv_combine_kernel<128>, dim3((unsigned)nwg), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((splitkv_combine_kernel<128, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p);
   else
-    hipLaunchKernelGGL(splitkv_combine_kernel<256>, dim3((unsigned)nwg), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((splitkv_combine_kernel<256, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p);
   return (int)hipGetLastError();
 }
 

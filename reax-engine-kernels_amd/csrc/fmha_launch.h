@@ -40,6 +40,21 @@ struct SplitParams {
 size_t splitkv_workspace_bytes(int B, int H, int M, int head_dim, int num_splits);
 int launch_splitkv(const SplitParams& p, int head_dim, hipStream_t stream);
 
+// The decode kernel + combine kernel on a prepared FwdParams whose num_splits, split_len (a multiple of P key tiles:
+// 64 keys at head_dim 128, 32 at 256), ws_o and ws_lse are set; P = 1, 2 or 4 wavefronts per split, p.M <= 32.
+// post: the combine applies reax_fmha_qp's gate epilogue (head_dim 256) instead of storing O / LSE.
+int launch_decode_split(FwdParams p, int head_dim, int P, bool post, hipStream_t stream);
+// Points p.ws_o / p.ws_lse into a workspace laid out as splitkv_workspace_bytes describes (p.num_splits set).
+void set_workspace(FwdParams& p, void* ws, int head_dim);
+
+// The drop-in entry points at short query blocks (head_dim 256, qpos mode, at most 32 folded rows per (b, KV
+// head), e.g. one decode token of 8 query heads): split-KV through the library's static per-device scratch, with
+// the split count chosen to fill the GPU (fmha_short.hip). Returns SHORT_NOT_TAKEN when the call should run
+// unsplit instead (short key ranges, a stream being captured, the scratch in use by another stream's unfinished
+// call, a shape whose partials exceed a scratch slot), else 0 or a hipError_t code.
+constexpr int SHORT_NOT_TAKEN = -1000;
+int launch_short_split(const FwdParams& p, bool post, hipStream_t stream);
+
 // The same with the library's per-device static scratch as the workspace (p.ws / p.ws_bytes are ignored): no
 // allocation anywhere on the call path. Returns hipErrorOutOfMemory when the workspace the shape needs exceeds
 // SPLITKV_SCRATCH_BYTES (fmha_noalloc.hip).

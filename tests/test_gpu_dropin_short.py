@@ -120,7 +120,7 @@ SHORT = [
 def test_reax_fmha_q_short(lib, shape):
     B, S, G, Hkv, N, lens = shape
     qp = decode_qpos(B, S, N, lens)
-    c = FC.Case(f"q_short_{lib}", B=B, S=S, N=N, Hq=G * Hkv, Hkv=Hkv, D=256, mode="qpos", seed=500 + S * G + N,
+    c = FC.Case(f"q_short_{lib}", B=B, S=S, N=N, Hq=G * Hkv, Hkv=Hkv, D=256, mode="qpos", seed=500 + S * G + N % 997,
                 qpos=qp)
     _say(f"reax_fmha_q {lib} B{B} S{S} G{G} Hkv{Hkv} N{N} (M = {S * G})")
     a = FC.build(c)
@@ -228,3 +228,132 @@ def test_varlen_d256_short():
     torch.cuda.synchronize()
     ref_o, ref_lse = FC.oracle_ref(c, a)
     FC.check_tolerance(W.torch_to_bits(o), ref_o, lse.cpu().numpy(), ref_lse, where=c.name)
+
+
+# ---------------------------------------------------------------------------------------- split-KV behind the ABI
+# At most 32 folded rows and long enough key ranges, reax_fmha_q / reax_fmha_qp split the keys across the GPU
+# (fmha_short.hip: the decode kernel per split, partials in the library's static scratch, an LSE combine that
+# applies the entry point's store). These shapes take that path; the cache lengths differ per batch entry, so
+# some splits see no key at all, and one entry's cache holds one key (the block rule: V[0]).
+
+SPLIT = [
+    (1, 1, 8, 2, 32768, None),                     # the bench's batch-1 decode step
+    (2, 4, 8, 1, 9000, [9000, 4500]),              # M = 32: four tokens of 8 heads
+    (4, 1, 16, 2, 3000, [3000, 1, 2999, 64]),      # G = 16
+    (3, 3, 8, 2, 20000, [20000, 2, 7777]),         # M = 24, a two-key cache
+]
+
+
+@pytest.mark.parametrize("lib", ["howu", "post"])
+@pytest.mark.parametrize("shape", SPLIT, ids=lambda s: f"B{s[0]}_S{s[1]}_G{s[2]}_H{s[3]}_N{s[4]}")
+def test_reax_fmha_q_split(lib, shape):
+    test_reax_fmha_q_short(lib, shape)
+
+
+@pytest.mark.parametrize("qmode", ["decode", "beyond"])
+def test_reax_fmha_qp_split(qmode):
+    """reax_fmha_qp on the split path, B 5 decode steps over a 12000-key cache: per-entry cache lengths ('decode'),
+    or qpos past the cache's end for some entries (they see every key) and -1 for one (nothing: O = 0)."""
+    N, B = 12000, 5
+    qp = decode_qpos(B, 1, N, [12000, 1, 6000, 130, 11999]) if qmode == "decode" else \
+        np.array([[N + 5], [-1], [N - 1], [2 * N], [0]], dtype=np.int32)
+    c = FC.Case(f"qp_split_{qmode}", B=B, S=1, N=N, Hq=16, Hkv=2, D=256, mode="qpos", seed=571, qpos=qp)
+    _say(f"reax_fmha_qp split {qmode} B{B} N{N}")
+    a = FC.build(c)
+    inv, qg, T = _post_case(c, a, 572, drop=[(3, 0)])
+    got = run_qp(c, a, qg, inv, T)
+    o, _ = FC.oracle_ref(c, a, dropin=True)
+    want = np.full((T, c.Hq * c.D), 0x7E00, dtype=np.uint16)
+    of = o.reshape(c.B, c.S, c.Hkv, c.G, c.D).transpose(0, 2, 1, 3, 4).reshape(c.B, c.Hkv, c.S * c.G, c.D)
+    pyoracle.post_gate(of, B=c.B, H=c.Hkv, G=c.G, M=c.S * c.G, D=c.D, inv=inv, Lq=c.S, qg=qg,
+                       qg_rs=c.Hq * 2 * c.D, out=want, out_rs=c.Hq * c.D)
+    untouched = np.setdiff1d(np.arange(T), inv[inv >= 0])
+    assert (got[untouched] == 0x7E00).all(), "rows not named by inv must stay untouched"
+    rows = inv[inv >= 0]
+    FC.check_tolerance(got[rows], W.bf16_bits_to_f32(want[rows]).astype(np.float64), where=c.name)
+    for b in range(B):
+        R = inv[b, 0]
+        if R >= 0 and (a["qpos"][b, 0] <= 0):  # V[0] (block rule) or 0: exact
+            assert (got[R] == want[R]).all(), f"{c.name}: entry {b} not bit-exact"
+
+
+def test_short_split_two_streams():
+    """Calls on two streams share the library's split scratch: each stream's calls are queued without host
+    synchronisation, alternating, into separate outputs; every output must equal the same call made alone on the
+    default stream, bit for bit (the split path is deterministic)."""
+    from reax_fmha import ops
+
+    N, B, G, Hkv = 6000, 3, 8, 2
+    cases = []
+    for i in range(6):
+        c = FC.Case(f"streams_{i}", B=B, S=1, N=N, Hq=G * Hkv, Hkv=Hkv, D=256, mode="qpos", seed=580 + i,
+                    qpos=decode_qpos(B, 1, N, [N - 7 * i, N // (i + 1), 100 * i + 1]))
+        a = FC.build(c)
+        q = dev(fold(a["q"], G))
+        cases.append((c, q, dev(a["k"]), dev(a["v"]), torch.from_numpy(a["qpos"]).cuda()))
+    _say("split scratch shared by two streams")
+    alone = []
+    for c, q, k, v, qpos in cases:
+        o = torch.empty_like(q)
+        ops.fmha_q(q, k, v, qpos, G, o, c.scale, lib="post")
+        alone.append(o)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for i, (c, q, k, v, qpos) in enumerate(cases):
+        with torch.cuda.stream(s1 if i % 2 == 0 else s2):
+            o = torch.full_like(q, float("nan"))
+            ops.fmha_q(q, k, v, qpos, G, o, c.scale, lib="post")
+            outs.append(o)
+    torch.cuda.synchronize()
+    for i, (o, ref) in enumerate(zip(outs, alone)):
+        assert torch.equal(o.view(torch.int16), ref.view(torch.int16)), f"call {i} differs from the same call alone"
+    c, q, k, v, qpos = cases[0]
+    a = FC.build(c)
+    oref, _ = FC.oracle_ref(c, a, dropin=True)
+    FC.check_tolerance(unfold(W.torch_to_bits(outs[0]), G), oref, where="two streams")
+
+
+def test_short_split_graph_capture():
+    """Under graph capture the drop-in entry point runs unsplit (the capture must not depend on the split scratch
+    or its events); the captured call replays correctly on new inputs, and eager calls between the replays still
+    take the split path."""
+    from reax_fmha import ops
+
+    N, B, G, Hkv = 5000, 2, 8, 2
+    c = FC.Case("graph_short", B=B, S=1, N=N, Hq=G * Hkv, Hkv=Hkv, D=256, mode="qpos", seed=590,
+                qpos=decode_qpos(B, 1, N, [N, 3000]))
+    a = FC.build(c)
+    q, k, v = dev(fold(a["q"], G)), dev(a["k"]), dev(a["v"])
+    qpos = torch.from_numpy(a["qpos"]).cuda()
+    o = torch.empty_like(q)
+    run = lambda: ops.fmha_q(q, k, v, qpos, G, o, c.scale, lib="howu")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    torch.cuda.synchronize()
+    for i, seed in enumerate([591, 592, 593]):
+        _say(f"graph replay {i} seed {seed}")
+        ci = FC.Case("graph_short", B=B, S=1, N=N, Hq=G * Hkv, Hkv=Hkv, D=256, mode="qpos", seed=seed,
+                     qpos=c.qpos)
+        ai = FC.build(ci)
+        q.copy_(dev(fold(ai["q"], G)))
+        k.copy_(dev(ai["k"]))
+        v.copy_(dev(ai["v"]))
+        g.replay()
+        torch.cuda.synchronize()
+        got = unfold(W.torch_to_bits(o), G)
+        eager = torch.empty_like(q)
+        ops.fmha_q(q, k, v, qpos, G, eager, c.scale, lib="howu")
+        torch.cuda.synchronize()
+        oref, _ = FC.oracle_ref(ci, ai, dropin=True)
+        FC.check_tolerance(got, oref, where=f"replay {i}")
+        FC.check_tolerance(unfold(W.torch_to_bits(eager), G), oref, where=f"eager {i}")
