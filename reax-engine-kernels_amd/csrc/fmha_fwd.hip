@@ -825,12 +825,6 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   const int wmin = __builtin_amdgcn_readfirstlane(wave_min(lim));
   const int t_beg = wbeg / T::BN, t_end = wmax < wbeg ? t_beg : wmax / T::BN + 1;
 
-  const uint16_t* qrow = p.q + (long long)b * p.qsB + (long long)hk * p.qsH + (long long)tok * p.qsT + (long long)g * p.qsG;
-  bf16x8_t qf[T::QK];
-#pragma unroll
-  for (int ks = 0; ks < T::QK; ++ks)
-    qf[ks] = as_bf16x8(rvalid ? ld16(qrow + 16 * ks + 8 * hf) : u32x4_t{0u, 0u, 0u, 0u});
-  __builtin_amdgcn_s_waitcnt(vmcnt_le(0));  // Q has landed before the (untracked) tile loads start
   const uint16_t* Kb = p.k + (long long)b * p.ksB + (long long)hk * p.ksH;
   const uint16_t* Vb = p.v + (long long)b * p.vsB + (long long)hk * p.vsH;
   const Dma<HD, 1, T::BN> kplan(p.ksM, 0, lane), vplan(p.vsM, 0, lane);
@@ -842,6 +836,15 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   constexpr int DW = Dma<HD, 1, T::BN>::DW;
   uint8_t* kb_ = L.k[w];
   uint8_t* vb_ = L.v[w];
+  // the first K tile, then Q, then the first V tile: one memory latency for all three. Loads return in issue order,
+  // so the explicit wait for K(t_beg) before the first S^T (at most the V tile's DW loads outstanding) also covers
+  // Q; the waits the compiler adds for Q, which does not count the tile loads, are only stricter.
+  if (t_end > t_beg) kplan.template tile<2>(kb_, Kb, p.ksM, kfast, t_beg * T::BN, wend, 0, lane);
+  const uint16_t* qrow = p.q + (long long)b * p.qsB + (long long)hk * p.qsH + (long long)tok * p.qsT + (long long)g * p.qsG;
+  bf16x8_t qf[T::QK];
+#pragma unroll
+  for (int ks = 0; ks < T::QK; ++ks)
+    qf[ks] = as_bf16x8(rvalid ? ld16(qrow + 16 * ks + 8 * hf) : u32x4_t{0u, 0u, 0u, 0u});
 
   f32x16_t o[T::DB];
 #pragma unroll
@@ -853,10 +856,7 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   f32x16_t s[T::NKB];
   uint32_t pk[T::NKB][8];
 
-  if (t_end > t_beg) {
-    kplan.template tile<2>(kb_, Kb, p.ksM, kfast, t_beg * T::BN, wend, 0, lane);
-    vplan.template tile<2>(vb_, Vb, p.vsM, vfast, t_beg * T::BN, wend, 0, lane);
-  }
+  if (t_end > t_beg) vplan.template tile<2>(vb_, Vb, p.vsM, vfast, t_beg * T::BN, wend, 0, lane);
   for (int t = t_beg; t < t_end; ++t) {
     const int k0 = t * T::BN;
     const bool more = t + 1 < t_end;
@@ -966,10 +966,12 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   }
 }
 
-// LSE-weighted merge of the split partials: one wavefront per (b, kv head, row).
+// LSE-weighted merge of the split partials: one workgroup of 4 wavefronts per (b, kv head, row).
 //   lse = log(sum_s exp(lse_s)),  O = sum_s exp(lse_s - lse) * O_s     (O_s already normalised by its row sum)
-// Lane s holds split s's weight (64 splits per pass) and the partial rows are read in batches of 8 independent
-// loads per lane, so a row costs a few memory round trips rather than one per split.
+// Wavefront w merges splits w, w + 4, w + 8, ...: lane j holds the LSE of its j-th split (64 per pass), the
+// wavefronts' maxima meet in LDS, and the partial rows are read in batches of BATCH independent loads per lane (the
+// first batch issued before the LSEs are known), so a row costs two or three memory round trips rather than one per
+// split; the four wavefronts' sums meet in LDS again.
 __device__ __forceinline__ float wave_maxf(float x) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
@@ -981,53 +983,82 @@ __device__ __forceinline__ float wave_sumf(float x) {
   return x;
 }
 
+constexpr int CMB_NW = 4;  // wavefronts per row of the combine kernel
+
 // POST: the drop-in reax_fmha_qp's epilogue instead of the O / LSE store (reax_fmha_v11.cu:451-522): O rounded to
 // bf16, times the bf16 sigmoid of the gate qg[R][hq][HD + d], rounded once, stored to out[R][hq * HD + d] for the
 // token row R = inv[b * Lq + token]; rows with R < 0 are left untouched.
 template <int HD, bool POST>
-__global__ void __launch_bounds__(256) splitkv_combine_kernel(const FwdParams p) {
+__global__ void __launch_bounds__(64 * CMB_NW) splitkv_combine_kernel(const FwdParams p) {
   constexpr int DPL = HD / 64;  // dims per lane
   constexpr int BATCH = 16;
-  const long long wid = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (wid >= (long long)p.B * p.H * p.M) return;
-  const int r = (int)(wid % p.M);
-  const long long bh = wid / p.M;
+  __shared__ float red[CMB_NW][DPL][64];
+  __shared__ float rsum[CMB_NW], rmax[CMB_NW];
+  const long long row_id = blockIdx.x;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int r = (int)(row_id % p.M);
+  const long long bh = row_id / p.M;
   const int b = (int)(bh / p.H), hk = (int)(bh % p.H);
   const int S = p.num_splits;
-  const long long base = bh * S * p.M + r;  // split s's partial row: base + s * M
-  float mx = -INFINITY;
-  for (int s0 = 0; s0 < S; s0 += 64)
-    if (s0 + lane < S) mx = fmaxf(mx, p.ws_lse[base + (long long)(s0 + lane) * p.M]);
-  mx = wave_maxf(mx);
+  const long long base = bh * S * p.M + r;                  // split s's partial row: base + s * M
+  const int Sw = S > w ? (S - w + CMB_NW - 1) / CMB_NW : 0;  // this wavefront's splits: w + CMB_NW j, j < Sw
+  auto prow = [&](int j) -> const float* {
+    return p.ws_o + (base + (long long)(w + CMB_NW * j) * p.M) * HD + DPL * lane;
+  };
+  auto load_batch = [&](float (&v)[BATCH][DPL], int i0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+      const float* po = prow(min(i0 + i, Sw - 1));  // past the end: a clamped (in-bounds) row, weighted 0
+      if constexpr (DPL == 4) {
+        const f32x4_t x = *reinterpret_cast<const f32x4_t*>(po);
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) v[i][e] = x[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) v[i][e] = po[e];
+      }
+    }
+  };
+  float v[BATCH][DPL];
+  if (Sw > 0) load_batch(v, 0);
+  float l0 = lane < Sw ? p.ws_lse[base + (long long)(w + CMB_NW * lane) * p.M] : -INFINITY;
+  float mloc = l0;
+  for (int j0 = 64; j0 < Sw; j0 += 64)
+    if (j0 + lane < Sw) mloc = fmaxf(mloc, p.ws_lse[base + (long long)(w + CMB_NW * (j0 + lane)) * p.M]);
+  mloc = wave_maxf(mloc);
+  if (lane == 0) rmax[w] = mloc;
+  __syncthreads();
+  const float mx = fmaxf(fmaxf(rmax[0], rmax[1]), fmaxf(rmax[2], rmax[3]));
   float acc[DPL];
 #pragma unroll
   for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
   float wsum = 0.f;
   if (mx != -INFINITY) {
-    for (int s0 = 0; s0 < S; s0 += 64) {
-      const int n = min(64, S - s0);
-      const float wl = lane < n ? fast_exp2((p.ws_lse[base + (long long)(s0 + lane) * p.M] - mx) * 1.44269504088896340736f)
-                                : 0.f;
+    for (int j0 = 0; j0 < Sw; j0 += 64) {
+      const int n = min(64, Sw - j0);
+      const float lv = j0 == 0 ? l0 : (lane < n ? p.ws_lse[base + (long long)(w + CMB_NW * (j0 + lane)) * p.M] : -INFINITY);
+      const float wl = lane < n ? fast_exp2((lv - mx) * 1.44269504088896340736f) : 0.f;
       wsum += wl;
-      for (int j0 = 0; j0 < n; j0 += BATCH) {
-        float v[BATCH][DPL], wj[BATCH];
+      for (int i0 = 0; i0 < n; i0 += BATCH) {
+        if (j0 + i0 > 0) load_batch(v, j0 + i0);
 #pragma unroll
-        for (int j = 0; j < BATCH; ++j) {
-          const int jj = min(j0 + j, n - 1);  // a clamped (in-bounds) row whose weight is zeroed below
-          const float* po = p.ws_o + (base + (long long)(s0 + jj) * p.M) * HD + DPL * lane;
+        for (int i = 0; i < BATCH; ++i) {
+          const float wi = i0 + i < n ? __shfl(wl, min(i0 + i, 63), 64) : 0.f;
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) v[j][e] = po[e];
-          wj[j] = j0 + j < n ? __shfl(wl, jj, 64) : 0.f;
+          for (int e = 0; e < DPL; ++e) acc[e] += wi * v[i][e];
         }
-#pragma unroll
-        for (int j = 0; j < BATCH; ++j)
-#pragma unroll
-          for (int e = 0; e < DPL; ++e) acc[e] += wj[j] * v[j][e];
       }
     }
-    wsum = wave_sumf(wsum);
   }
+  wsum = wave_sumf(wsum);
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) red[w][e][lane] = acc[e];
+  if (lane == 0) rsum[w] = wsum;
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int e = 0; e < DPL; ++e) acc[e] = (red[0][e][lane] + red[1][e][lane]) + (red[2][e][lane] + red[3][e][lane]);
+  wsum = (rsum[0] + rsum[1]) + (rsum[2] + rsum[3]);
   const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
   const int tok = r / p.G, g = r - tok * p.G;
   if (POST) {
@@ -1173,9 +1204,8 @@ int launch_decode_split(FwdParams p, int head_dim, int P, bool post, hipStream_t
   const long long ntask = (long long)p.B * p.H * p.num_splits;
   const long long nwg = (ntask + (DEC_NW / P) - 1) / (DEC_NW / P);
   if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
-  const long long nrow = (long long)p.B * p.H * p.M;
-  const long long cwg = (nrow + 3) / 4;
-  if (cwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  const long long cwg = (long long)p.B * p.H * p.M;  // one combine workgroup per row
+  if (cwg <= 0 || cwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
   if (head_dim == 128) {
     if (post || p.qpos0_block) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL((fmha_decode_kernel<128, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
@@ -1186,11 +1216,11 @@ int launch_decode_split(FwdParams p, int head_dim, int P, bool post, hipStream_t
   }
   if (const int rc = (int)hipGetLastError()) return rc;
   if (head_dim == 128)
-    hipLaunchKernelGGL((splitkv_combine_kernel<128, false>), dim3((unsigned)cwg), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((splitkv_combine_kernel<128, false>), dim3((unsigned)cwg), dim3(64 * CMB_NW), 0, stream, p);
   else if (post)
-    hipLaunchKernelGGL((splitkv_combine_kernel<256, true>), dim3((unsigned)cwg), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((splitkv_combine_kernel<256, true>), dim3((unsigned)cwg), dim3(64 * CMB_NW), 0, stream, p);
   else
-    hipLaunchKernelGGL((splitkv_combine_kernel<256, false>), dim3((unsigned)cwg), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((splitkv_combine_kernel<256, false>), dim3((unsigned)cwg), dim3(64 * CMB_NW), 0, stream, p);
   return (int)hipGetLastError();
 }
 
@@ -1222,13 +1252,12 @@ int launch_splitkv(const SplitParams& sp, int head_dim, hipStream_t stream) {
          : head_dim == 256 ? launch_fwd_t<256, MODE_QPOS, false, true>(p, stream)
                            : (int)hipErrorInvalidValue;
   if (rc) return rc;
-  const long long nrow = (long long)p.B * p.H * p.M;
-  const long long nwg = (nrow + 3) / 4;
-  if (nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  const long long nwg = (long long)p.B * p.H * p.M;  // one combine workgroup per row
+  if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
   if (head_dim == 128)
-    hipLaunchKernelGGL((splitkv_combine_kernel<128, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((splitkv_combine_kernel<128, false>), dim3((unsigned)nwg), dim3(64 * CMB_NW), 0, stream, p);
   else
-    hipLaunchKernelGGL((splitkv_combine_kernel<256, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((splitkv_combine_kernel<256, false>), dim3((unsigned)nwg), dim3(64 * CMB_NW), 0, stream, p);
   return (int)hipGetLastError();
 }
 

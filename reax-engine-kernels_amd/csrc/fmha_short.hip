@@ -9,13 +9,13 @@
 //
 // The split partials need device memory the drop-in ABI has no argument for, and the reference allocates nothing.
 // They go to `short_scratch`, a file-scope device array (SHORT_SLOTS slots of SHORT_SLOT_BYTES; each GPU the
-// library runs on holds its own copy until the process ends). Calls on one GPU share it, so every use is ordered
-// on the GPU after the previous use of its slot: the call's stream waits on the slot's event (recorded on the
-// stream of the slot's previous call) before the split kernel, and records it again after the combine. Calls on
-// one stream are ordered anyway; calls on different streams take a slot last used by their own stream, else one
-// whose last use has finished, else they queue behind the least recently used one. Nothing is allocated on the
-// call path after a slot's event has been created (once per slot and device); a stream under graph capture, a
-// short key range or a shape whose partials exceed a slot runs the unsplit kernel instead.
+// library runs on holds its own copy until the process ends). Calls on one GPU share it, so every use of a slot is
+// ordered on the GPU after its previous use: each call's stream waits on the slot's event before the split kernel
+// and records it again after the combine kernel. A call takes the slot last used by a stream with its handle (the
+// wait is then within one stream), else a slot whose last use has finished, else the least recently used slot
+// (its stream then queues behind that use). Nothing is allocated on the call path after a slot's event has been
+// created (once per slot and device); a stream under graph capture, a short key range or a shape whose partials
+// exceed a slot runs the unsplit kernel instead.
 #include <hip/hip_runtime.h>
 
 #include <climits>
@@ -39,8 +39,8 @@ struct DeviceSlots {
   std::mutex mu;
   uint8_t* base = nullptr;  // device address of short_scratch on this device, once looked up
   bool lookup_failed = false;
-  hipStream_t owner[SHORT_SLOTS] = {};
-  hipEvent_t done[SHORT_SLOTS] = {};  // recorded on owner[i] after slot i's last use
+  unsigned long long owner[SHORT_SLOTS] = {};  // handle of the stream of slot i's last use
+  hipEvent_t done[SHORT_SLOTS] = {};          // recorded on that stream after slot i's last use
   unsigned long long last[SHORT_SLOTS] = {};
   unsigned long long tick = 0;
 };
@@ -102,6 +102,7 @@ int launch_short_split(const FwdParams& p0, bool post, hipStream_t stream) {
   int dev = -1;
   if ((stream ? hipStreamGetDevice(stream, &dev) : hipGetDevice(&dev)) != hipSuccess || dev < 0 || dev >= 64)
     return SHORT_NOT_TAKEN;
+  const unsigned long long sid = (unsigned long long)reinterpret_cast<uintptr_t>(stream);
   DeviceSlots& d = g_slots[dev];
   std::lock_guard<std::mutex> lock(d.mu);
   uint8_t* base = scratch_base(d, dev);
@@ -109,7 +110,7 @@ int launch_short_split(const FwdParams& p0, bool post, hipStream_t stream) {
   // a slot last used on this stream, else one whose last use has finished, else the least recently used one
   int slot = -1;
   for (int i = 0; i < SHORT_SLOTS && slot < 0; ++i)
-    if (d.done[i] && d.owner[i] == stream) slot = i;
+    if (d.done[i] && d.owner[i] == sid) slot = i;
   for (int i = 0; i < SHORT_SLOTS && slot < 0; ++i)
     if (!d.done[i] || hipEventQuery(d.done[i]) == hipSuccess) slot = i;
   if (slot < 0) {
@@ -121,7 +122,9 @@ int launch_short_split(const FwdParams& p0, bool post, hipStream_t stream) {
     d.done[slot] = nullptr;
     return SHORT_NOT_TAKEN;
   }
-  // order this use after the slot's previous one, whichever stream it ran on (a no-op once that has finished)
+  // always wait, also when the slot's last use was on a stream with this handle: a handle can name a new stream
+  // after the old one was destroyed with work pending, and the wait costs nothing measurable (the ~6 us between a
+  // preceding kernel and the split kernel in a kernel trace is there with or without it)
   if (const int rc = (int)hipStreamWaitEvent(stream, d.done[slot], 0)) return rc;
   FwdParams p = p0;
   p.num_splits = splits;
@@ -129,7 +132,7 @@ int launch_short_split(const FwdParams& p0, bool post, hipStream_t stream) {
   set_workspace(p, base + (size_t)slot * SHORT_SLOT_BYTES, 256);
   if (const int rc = launch_decode_split(p, 256, P, post, stream)) return rc;
   if (const int rc = (int)hipEventRecord(d.done[slot], stream)) return rc;
-  d.owner[slot] = stream;
+  d.owner[slot] = sid;
   d.last[slot] = ++d.tick;
   return 0;
 }

@@ -43,6 +43,22 @@ def test_reference_names_present():
     assert abi.POST_SYMBOLS == ["reax_fmha_b", "reax_fmha_q", "reax_fmha_qp"]
 
 
+@pytest.mark.parametrize("path", [abi.HOWU_PATH, abi.POST_PATH, abi.PLAIN_PATH, abi.SLICES_PATH, abi.GV_PATH])
+def test_hip_imports_resolve_in_torch_runtime(path):
+    # The libraries are loaded into processes whose HIP runtime may be an older one (torch's bundled
+    # libamdhip64.so, loaded first): every versioned HIP symbol they import must be defined there, or dlopen fails
+    torch = pytest.importorskip("torch")
+    rt = os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so")
+    if not os.path.exists(rt):
+        pytest.skip("torch has no bundled HIP runtime")
+    nm = lambda *a: subprocess.run(["nm", "-D", *a], check=True, capture_output=True, text=True).stdout
+    have = {line.split()[-1].replace("@@", "@") for line in nm("--defined-only", rt).splitlines()}
+    need = [line.split()[-1] for line in nm("--undefined-only", path).splitlines() if "@hip_" in line]
+    assert need, "no HIP imports found"
+    missing = [sym for sym in need if sym not in have]
+    assert not missing, f"{os.path.basename(path)} imports HIP symbols torch's runtime lacks: {missing}"
+
+
 @pytest.mark.parametrize("path", [abi.HOWU_PATH, abi.POST_PATH])
 def test_no_soname(path):
     out = subprocess.run(["readelf", "-d", path], check=True, capture_output=True, text=True).stdout
