@@ -966,12 +966,13 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   }
 }
 
-// LSE-weighted merge of the split partials: one workgroup of 4 wavefronts per (b, kv head, row).
+// LSE-weighted merge of the split partials: NW = 1 or 4 wavefronts per (b, kv head, row), 4 / NW rows per workgroup.
 //   lse = log(sum_s exp(lse_s)),  O = sum_s exp(lse_s - lse) * O_s     (O_s already normalised by its row sum)
-// Wavefront w merges splits w, w + 4, w + 8, ...: lane j holds the LSE of its j-th split (64 per pass), the
-// wavefronts' maxima meet in LDS, and the partial rows are read in batches of BATCH independent loads per lane (the
-// first batch issued before the LSEs are known), so a row costs two or three memory round trips rather than one per
-// split; the four wavefronts' sums meet in LDS again.
+// Wavefront w of a row merges splits w, w + NW, w + 2 NW, ...: lane j holds the LSE of its j-th split (64 per pass),
+// the wavefronts' maxima meet in LDS, and the partial rows are read in batches of BATCH independent loads per lane
+// (the first batch issued before the LSEs are known), so a row costs two or three memory round trips rather than one
+// per split; the wavefronts' sums meet in LDS again. Four wavefronts per row pay when there are many splits (the
+// drop-in decode at batch 1: 128 splits, 7.5 us against 13 us with one), one when there are few (config 4: 16).
 __device__ __forceinline__ float wave_maxf(float x) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, 64));
@@ -983,19 +984,22 @@ __device__ __forceinline__ float wave_sumf(float x) {
   return x;
 }
 
-constexpr int CMB_NW = 4;  // wavefronts per row of the combine kernel
+constexpr int CMB_WAVES = 4;  // wavefronts per workgroup of the combine kernel
 
 // POST: the drop-in reax_fmha_qp's epilogue instead of the O / LSE store (reax_fmha_v11.cu:451-522): O rounded to
 // bf16, times the bf16 sigmoid of the gate qg[R][hq][HD + d], rounded once, stored to out[R][hq * HD + d] for the
 // token row R = inv[b * Lq + token]; rows with R < 0 are left untouched.
-template <int HD, bool POST>
-__global__ void __launch_bounds__(64 * CMB_NW) splitkv_combine_kernel(const FwdParams p) {
+template <int HD, bool POST, int CMB_NW>
+__global__ void __launch_bounds__(64 * CMB_WAVES) splitkv_combine_kernel(const FwdParams p) {
+  static_assert(CMB_NW == 1 || CMB_NW == CMB_WAVES, "one or all wavefronts of the workgroup per row");
   constexpr int DPL = HD / 64;  // dims per lane
   constexpr int BATCH = 16;
-  __shared__ float red[CMB_NW][DPL][64];
-  __shared__ float rsum[CMB_NW], rmax[CMB_NW];
-  const long long row_id = blockIdx.x;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __shared__ float red[CMB_WAVES][DPL][64];
+  __shared__ float rsum[CMB_WAVES], rmax[CMB_WAVES];
+  const int lane = threadIdx.x & 63, wg = threadIdx.x >> 6;
+  const int w = wg % CMB_NW, w0 = wg - w;  // this wavefront's index within its row, the row's first wavefront
+  const long long row_id = (long long)blockIdx.x * (CMB_WAVES / CMB_NW) + wg / CMB_NW;
+  const bool live = row_id < (long long)p.B * p.H * p.M;
   const int r = (int)(row_id % p.M);
   const long long bh = row_id / p.M;
   const int b = (int)(bh / p.H), hk = (int)(bh % p.H);
@@ -1020,22 +1024,28 @@ __global__ void __launch_bounds__(64 * CMB_NW) splitkv_combine_kernel(const FwdP
     }
   };
   float v[BATCH][DPL];
-  if (Sw > 0) load_batch(v, 0);
-  float l0 = lane < Sw ? p.ws_lse[base + (long long)(w + CMB_NW * lane) * p.M] : -INFINITY;
+  const int Sl = live ? Sw : 0;  // a workgroup's last rows may lie past the end: they merge nothing
+  if (Sl > 0) load_batch(v, 0);
+  float l0 = lane < Sl ? p.ws_lse[base + (long long)(w + CMB_NW * lane) * p.M] : -INFINITY;
   float mloc = l0;
-  for (int j0 = 64; j0 < Sw; j0 += 64)
-    if (j0 + lane < Sw) mloc = fmaxf(mloc, p.ws_lse[base + (long long)(w + CMB_NW * (j0 + lane)) * p.M]);
+  for (int j0 = 64; j0 < Sl; j0 += 64)
+    if (j0 + lane < Sl) mloc = fmaxf(mloc, p.ws_lse[base + (long long)(w + CMB_NW * (j0 + lane)) * p.M]);
   mloc = wave_maxf(mloc);
-  if (lane == 0) rmax[w] = mloc;
-  __syncthreads();
-  const float mx = fmaxf(fmaxf(rmax[0], rmax[1]), fmaxf(rmax[2], rmax[3]));
+  float mx = mloc;
+  if constexpr (CMB_NW > 1) {
+    if (lane == 0) rmax[wg] = mloc;
+    __syncthreads();
+    mx = rmax[w0];
+#pragma unroll
+    for (int i = 1; i < CMB_NW; ++i) mx = fmaxf(mx, rmax[w0 + i]);
+  }
   float acc[DPL];
 #pragma unroll
   for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
   float wsum = 0.f;
   if (mx != -INFINITY) {
-    for (int j0 = 0; j0 < Sw; j0 += 64) {
-      const int n = min(64, Sw - j0);
+    for (int j0 = 0; j0 < Sl; j0 += 64) {
+      const int n = min(64, Sl - j0);
       const float lv = j0 == 0 ? l0 : (lane < n ? p.ws_lse[base + (long long)(w + CMB_NW * (j0 + lane)) * p.M] : -INFINITY);
       const float wl = lane < n ? fast_exp2((lv - mx) * 1.44269504088896340736f) : 0.f;
       wsum += wl;
@@ -1051,14 +1061,17 @@ __global__ void __launch_bounds__(64 * CMB_NW) splitkv_combine_kernel(const FwdP
     }
   }
   wsum = wave_sumf(wsum);
+  if constexpr (CMB_NW > 1) {
 #pragma unroll
-  for (int e = 0; e < DPL; ++e) red[w][e][lane] = acc[e];
-  if (lane == 0) rsum[w] = wsum;
-  __syncthreads();
-  if (w != 0) return;
+    for (int e = 0; e < DPL; ++e) red[wg][e][lane] = acc[e];
+    if (lane == 0) rsum[wg] = wsum;
+    __syncthreads();
+    if (w != 0) return;
 #pragma unroll
-  for (int e = 0; e < DPL; ++e) acc[e] = (red[0][e][lane] + red[1][e][lane]) + (red[2][e][lane] + red[3][e][lane]);
-  wsum = (rsum[0] + rsum[1]) + (rsum[2] + rsum[3]);
+    for (int e = 0; e < DPL; ++e) acc[e] = (red[w0][e][lane] + red[w0 + 1][e][lane]) + (red[w0 + 2][e][lane] + red[w0 + 3][e][lane]);
+    wsum = (rsum[w0] + rsum[w0 + 1]) + (rsum[w0 + 2] + rsum[w0 + 3]);
+  }
+  if (!live) return;
   const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
   const int tok = r / p.G, g = r - tok * p.G;
   if (POST) {
@@ -1200,12 +1213,32 @@ static void decode_split_shape(int head_dim, int N, int num_splits, int& P, int&
   split_len = ((qt + P - 1) / P) * P * BN;
 }
 
+// The combine kernel for p.num_splits splits: four wavefronts per row from 32 splits on, else one.
+static int launch_combine(const FwdParams& p, int head_dim, bool post, hipStream_t stream) {
+  const long long rows = (long long)p.B * p.H * p.M;
+  const bool wide = p.num_splits >= 32;
+  const long long nwg = wide ? rows : (rows + CMB_WAVES - 1) / CMB_WAVES;
+  if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  const dim3 grid((unsigned)nwg), block(64 * CMB_WAVES);
+  if (head_dim == 128 && !post) {
+    if (wide) hipLaunchKernelGGL((splitkv_combine_kernel<128, false, CMB_WAVES>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((splitkv_combine_kernel<128, false, 1>), grid, block, 0, stream, p);
+  } else if (head_dim == 256 && post) {
+    if (wide) hipLaunchKernelGGL((splitkv_combine_kernel<256, true, CMB_WAVES>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((splitkv_combine_kernel<256, true, 1>), grid, block, 0, stream, p);
+  } else if (head_dim == 256) {
+    if (wide) hipLaunchKernelGGL((splitkv_combine_kernel<256, false, CMB_WAVES>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((splitkv_combine_kernel<256, false, 1>), grid, block, 0, stream, p);
+  } else {
+    return (int)hipErrorInvalidValue;
+  }
+  return (int)hipGetLastError();
+}
+
 int launch_decode_split(FwdParams p, int head_dim, int P, bool post, hipStream_t stream) {
   const long long ntask = (long long)p.B * p.H * p.num_splits;
   const long long nwg = (ntask + (DEC_NW / P) - 1) / (DEC_NW / P);
   if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
-  const long long cwg = (long long)p.B * p.H * p.M;  // one combine workgroup per row
-  if (cwg <= 0 || cwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
   if (head_dim == 128) {
     if (post || p.qpos0_block) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL((fmha_decode_kernel<128, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
@@ -1215,13 +1248,7 @@ int launch_decode_split(FwdParams p, int head_dim, int P, bool post, hipStream_t
     hipLaunchKernelGGL((fmha_decode_kernel<256, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
   }
   if (const int rc = (int)hipGetLastError()) return rc;
-  if (head_dim == 128)
-    hipLaunchKernelGGL((splitkv_combine_kernel<128, false>), dim3((unsigned)cwg), dim3(64 * CMB_NW), 0, stream, p);
-  else if (post)
-    hipLaunchKernelGGL((splitkv_combine_kernel<256, true>), dim3((unsigned)cwg), dim3(64 * CMB_NW), 0, stream, p);
-  else
-    hipLaunchKernelGGL((splitkv_combine_kernel<256, false>), dim3((unsigned)cwg), dim3(64 * CMB_NW), 0, stream, p);
-  return (int)hipGetLastError();
+  return launch_combine(p, head_dim, post, stream);
 }
 
 void set_workspace(FwdParams& p, void* ws, int head_dim) {
@@ -1252,13 +1279,7 @@ int launch_splitkv(const SplitParams& sp, int head_dim, hipStream_t stream) {
          : head_dim == 256 ? launch_fwd_t<256, MODE_QPOS, false, true>(p, stream)
                            : (int)hipErrorInvalidValue;
   if (rc) return rc;
-  const long long nwg = (long long)p.B * p.H * p.M;  // one combine workgroup per row
-  if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
-  if (head_dim == 128)
-    hipLaunchKernelGGL((splitkv_combine_kernel<128, false>), dim3((unsigned)nwg), dim3(64 * CMB_NW), 0, stream, p);
-  else
-    hipLaunchKernelGGL((splitkv_combine_kernel<256, false>), dim3((unsigned)nwg), dim3(64 * CMB_NW), 0, stream, p);
-  return (int)hipGetLastError();
+  return launch_combine(p, head_dim, false, stream);
 }
 
 }  // namespace reax
