@@ -20,7 +20,8 @@
 // The row maxima of S(t) are computed at the end of the MFMA phase (while the P.V MFMAs run) and published at the
 // next barrier; the probabilities at the end of the softmax phase, for the partner's next MFMA phase. The softmax
 // phase is about half as long as an MFMA phase, so the direct-to-LDS tile loads (64 KB per step) are issued from
-// the softmax phases, where they cost no matrix-core time: K(t+1) by group 1 in half 1, V(t) by group 0 in half 2.
+// the softmax phases, where they cost no matrix-core time: K(t+1) by group 1 at the start of half 1, V(t) by group
+// 0 at the start of half 2; the MFMA phases run at a raised wave priority.
 // (Issued all in half 1, with group 1's softmax, they made that half longer than the MFMA phase opposite it:
 // config 5 ran 9.9 ms that way and 8.65 ms split.)
 #include "fmha_common.h"
@@ -227,12 +228,18 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pair_kernel(const FwdParams p
       const bool qk = t < t_end && t * T::BN <= wmax;
       using Y = std::true_type;
       using N = std::false_type;
+      // the MFMA phase at a raised wave priority: where the SIMD's two wavefronts compete for an issue slot, the
+      // one feeding the matrix core goes first, ahead of its partner's softmax and tile loads (config 5: 9.03 ->
+      // 8.74 ms, same box, alternated; the head_dim-128 kernel, whose loads go out from its MFMA phase, gains
+      // nothing from it)
+      __builtin_amdgcn_s_setprio(1);
       if (pv && qk)
         mfma_block(Y{}, Y{}, kb_t, vb_prev);
       else if (pv)
         mfma_block(Y{}, N{}, kb_t, vb_prev);
       else if (qk)
         mfma_block(N{}, Y{}, kb_t, vb_prev);
+      __builtin_amdgcn_s_setprio(0);
       if (qk) {
         const int k0 = t * T::BN + 32 * role;
         if (k0 + 31 > wmin) {  // the keys straddle some row's last visible key
@@ -282,8 +289,8 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pair_kernel(const FwdParams p
       }
     };
     // the loads of step t, split over both halves so that the memory pipeline streams through the whole step:
-    // K(t+1) by group 1 in half 1 (after its softmax), V(t) by group 0 at the start of half 2 (before its
-    // softmax); both land before the end-of-step barrier
+    // K(t+1) by group 1 at the start of half 1, V(t) by group 0 at the start of half 2, each before its group's
+    // softmax; both land before the end-of-step barrier
     auto load_k = [&](int t) __attribute__((always_inline)) {
       if (t + 1 < t_end) tile_load(kring[(t + 1) & 1], Kb, p.ksM, kfast, (t + 1) * T::BN);
     };
@@ -301,8 +308,8 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pair_kernel(const FwdParams p
         if (grp == 0) {
           mfma_phase(t, kb_t, vb_prev);
         } else {
+          load_k(t);  // before the softmax: ~0.7% faster on config 5 than after it (the loads get longer to land)
           if (t >= 1) softmax(t - 1);
-          load_k(t);
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wavefront's xm / xp writes are visible ...
         exec_barrier();                      // ... to its partner after the barrier (the tile loads stay in flight)
