@@ -453,7 +453,8 @@ def test_config3_varlen():
     a = dict(q=q, k=k, v=v, cu=cu)
     og, lg = run_varlen(c, a)
     o, lse = FC.oracle_ref(c, a)
-    FC.check_tolerance(og, o, lg, lse, where="config3")
+    res = FC.check_tolerance(og, o, lg, lse, where="config3")
+    _say(f"  config 3 vs oracle (all rows): {res}")
 
 
 # ------------------------------------------------------------------------------------------ split-KV decode
@@ -577,7 +578,8 @@ def test_config4_decode():
     a = dict(q=q, k=k, v=v, qpos=qpos)
     og, lg = run_split(c, a, cfg.num_splits)
     o, lse = FC.oracle_ref(c, a)
-    FC.check_tolerance(og, o, lg, lse, where="config4")
+    res = FC.check_tolerance(og, o, lg, lse, where="config4")
+    _say(f"  config 4 vs oracle (all rows): {res}")
 
 
 # ------------------------------------------------------------------------------------------ full-size configs
@@ -591,7 +593,8 @@ def test_config2_prefill():
     og, lg = run_qx(c, a)
     toks = token_subset(cfg.S, 96, 7)
     o, lse = oracle_on_tokens(c, a, toks)
-    FC.check_tolerance(og[:, toks], o, lg[:, :, toks], lse, where="config2")
+    res = FC.check_tolerance(og[:, toks], o, lg[:, :, toks], lse, where="config2")
+    _say(f"  config 2 vs oracle ({len(toks)} tokens x all heads): {res}")
     res = torch_causal_check(og[0], lg[0], q, k, v, c.G, c.scale, where="config2")
     _say(f"  all {cfg.S} tokens vs float32: {res}")
 
@@ -617,7 +620,8 @@ def test_config5_post():
     pyoracle.post_gate(fold_dense(o, c.G), B=1, H=c.Hkv, G=c.G, M=len(toks) * c.G, D=c.D,
                        inv=np.arange(len(toks), dtype=np.int32), Lq=len(toks), qg=sub_qg, qg_rs=cfg.Hq * 2 * cfg.D,
                        out=want, out_rs=cfg.Hq * cfg.D)
-    FC.check_tolerance(got[toks], W.bf16_bits_to_f32(want).astype(np.float64), where="config5")
+    res = FC.check_tolerance(got[toks], W.bf16_bits_to_f32(want).astype(np.float64), where="config5")
+    _say(f"  config 5 vs oracle ({len(toks)} tokens x all heads, gated): {res}")
     res = torch_causal_check(got.reshape(T, cfg.Hq, cfg.D), None, q, k, v, c.G, c.scale,
                              gate_bits=qg[:, :, cfg.D:], where="config5")
     _say(f"  all {T} tokens vs float32: {res}")
