@@ -58,10 +58,15 @@ def pmc_traffic(path):
 
 def time_launches(torch, run, warm, iters):
     """Per-launch durations (ms) from HIP events recorded around each call on torch's current stream, the stream
-    the wrappers pass to the C ABI; `warm` untimed calls first."""
+    the wrappers pass to the C ABI; `warm` untimed calls first. The timed calls queue behind a GPU spin of about
+    50 us per call, so the GPU reaches them back to back: a launch through ctypes plus two event records takes the
+    host ~15 us, longer than the smallest kernels (config 1: ~11 us), and without the spin the GPU would wait for
+    the host between the events and the gap would count as kernel time."""
     for _ in range(warm):
         run()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(iters * 50e-6 * 2.1e9))  # clock cycles at ~2.1 GHz
     for a, b in evs:
         a.record()
         run()

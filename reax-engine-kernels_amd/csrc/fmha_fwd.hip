@@ -775,6 +775,10 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
 // A tile is 16 KB at either head dim: 64 keys at head_dim 128, 32 keys at head_dim 256.
 // BLK0: the drop-in entry points' block rule (all rows of (b, h) form one block of at most 32 rows: when the
 // largest raw qpos among them is 0, every live row sees key 0 only, reax_fmha_v8.cu:155-162, 224-235).
+// ROWS: a prefill too small to fill the GPU with 256-row items (reax_fmha_qx at S 512: 16 items for 256 CUs).
+// The task is then a 32-row block (b, block, KV head) of any p.M, blocks with the most keys first; the workgroup's
+// 4 wavefronts cut the block's key range [0, its largest key limit] into 4 runs of whole tiles, and the merge
+// through LDS writes the final O (bf16, 16-byte stores when o_vec8) and LSE instead of split partials.
 constexpr int DEC_NW = 4;
 
 template <int HD>
@@ -787,8 +791,9 @@ struct DecTile {
   static_assert(TILE == 16384, "two 16 KB tiles per wavefront, four wavefronts: 128 KB of LDS");
 };
 
-template <int HD, bool BLK0>
-__global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, int wpsplit) {
+template <int HD, bool BLK0, bool ROWS>
+__global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, int wpsplit, int o_vec8) {
+  static_assert(!(BLK0 && ROWS), "the block rule belongs to the drop-in decode");
   using T = DecTile<HD>;
   // the K and V tiles of the four wavefronts; after the key loop the same bytes hold the partials being merged
   // (DEC_NW x 32 rows x HD fp32: 64 KB at head_dim 128, all 128 KB at 256)
@@ -801,30 +806,26 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   __shared__ float mm[DEC_NW * 32], lm[DEC_NW * 32];
   const int tid = threadIdx.x, lane = tid & 63, hf = lane >> 5, lr = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wavefront-uniform: keeps the loop control scalar
-  const int P = wpsplit, part = w % P;
-  const long long ntask = (long long)p.B * p.num_splits * p.H;
+  const int P = ROWS ? DEC_NW : wpsplit, part = w % P;
+  const int nrb = ROWS ? (p.M + 31) / 32 : 1;  // 32-row blocks per (b, KV head)
+  const long long ntask = (long long)p.B * (ROWS ? nrb : p.num_splits) * p.H;
   const long long task = (long long)blockIdx.x * (DEC_NW / P) + w / P;
   const bool active = task < ntask;
   const long long tk = active ? task : 0;
-  const int hk = (int)(tk % p.H);
-  const int split = (int)((tk / p.H) % p.num_splits);
-  const int b = (int)(tk / ((long long)p.H * p.num_splits));
-  const int kbeg = split * p.split_len, kend = min(p.N, kbeg + p.split_len);
-  const int qlen = p.split_len / P;  // a multiple of the tile size
-  const int wbeg = kbeg + part * qlen, wend = min(kend, wbeg + qlen);
+  const int hk = ROWS ? (int)((unsigned)tk % (unsigned)p.H) : (int)(tk % p.H);
+  int split = 0, rb = 0, b = 0;
+  if (ROWS) {
+    const unsigned t32 = (unsigned)tk, bh = (unsigned)p.B * (unsigned)p.H;  // tk < B * nrb * H <= INT_MAX
+    b = (int)((t32 / (unsigned)p.H) % (unsigned)p.B);
+    rb = nrb - 1 - (int)(t32 / bh);
+  } else {
+    split = (int)((tk / p.H) % p.num_splits);
+    b = (int)(tk / ((long long)p.H * p.num_splits));
+  }
 
-  const int r = lr;  // row (folded: token r/G, head r%G); p.M <= 32
+  const int r = rb * 32 + lr;  // row (folded: token r/G, head r%G); without ROWS p.M <= 32 and rb = 0
   const bool rvalid = r < p.M;
   const int tok = rvalid ? r / p.G : 0, g = rvalid ? r - tok * p.G : 0;
-  int qr = -1;
-  if (rvalid && active) qr = p.qpos[(long long)b * p.qpBs + tok];
-  if (BLK0 && p.N > 0 && wave_max(qr) == 0 && rvalid) qr = 0;  // the block rule: every live row sees key 0
-  int lim = max(min(qr, wend - 1), -1);
-  if (lim < wbeg) lim = -1;
-  const int wmax = __builtin_amdgcn_readfirstlane(wave_max(lim));
-  const int wmin = __builtin_amdgcn_readfirstlane(wave_min(lim));
-  const int t_beg = wbeg / T::BN, t_end = wmax < wbeg ? t_beg : wmax / T::BN + 1;
-
   const uint16_t* Kb = p.k + (long long)b * p.ksB + (long long)hk * p.ksH;
   const uint16_t* Vb = p.v + (long long)b * p.vsB + (long long)hk * p.vsH;
   const Dma<HD, 1, T::BN> kplan(p.ksM, 0, lane), vplan(p.vsM, 0, lane);
@@ -834,17 +835,60 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   for (int kb = 0; kb < T::NKB; ++kb) kbase[kb] = k_lane_base<HD>(kb, lr, hf);
   const uint32_t vbase = v_lane_base<HD>(lane);
   constexpr int DW = Dma<HD, 1, T::BN>::DW;
+  // a decode split streams its keys once: nontemporal loads; the row blocks of one (b, KV head) all read the same
+  // tiles, which stay in L2 for the next block with ordinary loads
+  constexpr int LK = ROWS ? 1 : 2;
   uint8_t* kb_ = L.k[w];
   uint8_t* vb_ = L.v[w];
-  // the first K tile, then Q, then the first V tile: one memory latency for all three. Loads return in issue order,
-  // so the explicit wait for K(t_beg) before the first S^T (at most the V tile's DW loads outstanding) also covers
-  // Q; the waits the compiler adds for Q, which does not count the tile loads, are only stricter.
-  if (t_end > t_beg) kplan.template tile<2>(kb_, Kb, p.ksM, kfast, t_beg * T::BN, wend, 0, lane);
   const uint16_t* qrow = p.q + (long long)b * p.qsB + (long long)hk * p.qsH + (long long)tok * p.qsT + (long long)g * p.qsG;
   bf16x8_t qf[T::QK];
+  // tiles t_beg, t_beg + t_step, ... below t_end; keys above a row's lim are masked; tile loads stop at kend
+  int t_beg, t_end, t_step, kend, lim;
+  if (ROWS) {
+    // tiles part, part + P, ...: the first one does not depend on qpos, so Q, then its K and V, then qpos go out
+    // together (one memory latency; a block seeing fewer tiles leaves the tile unused). Loads complete in issue
+    // order: the wait the compiler puts before qpos's use covers Q and the tile too, and its wait for Q before
+    // the first S^T is then already met.
+    kend = p.N;
 #pragma unroll
-  for (int ks = 0; ks < T::QK; ++ks)
-    qf[ks] = as_bf16x8(rvalid ? ld16(qrow + 16 * ks + 8 * hf) : u32x4_t{0u, 0u, 0u, 0u});
+    for (int ks = 0; ks < T::QK; ++ks)
+      qf[ks] = as_bf16x8(rvalid ? ld16(qrow + 16 * ks + 8 * hf) : u32x4_t{0u, 0u, 0u, 0u});
+    if (part * T::BN < p.N) {
+      kplan.template tile<LK>(kb_, Kb, p.ksM, kfast, part * T::BN, kend, 0, lane);
+      vplan.template tile<LK>(vb_, Vb, p.vsM, vfast, part * T::BN, kend, 0, lane);
+    }
+    int qr = -1;
+    if (rvalid && active) qr = p.qpos[(long long)b * p.qpBs + tok];
+    lim = max(min(qr, p.N - 1), -1);
+    const int blim = wave_ext_dpp<true>(lim);
+    t_beg = part;
+    t_end = blim < 0 ? 0 : blim / T::BN + 1;  // key tiles any row of the block sees
+    t_step = P;
+  } else {
+    int qr = -1;
+    if (rvalid && active) qr = p.qpos[(long long)b * p.qpBs + tok];
+    if (BLK0 && p.N > 0 && wave_max(qr) == 0 && rvalid) qr = 0;  // the block rule: every live row sees key 0
+    const int kbeg = split * p.split_len;
+    kend = min(p.N, kbeg + p.split_len);
+    const int qlen = p.split_len / P;  // a multiple of the tile size
+    const int wbeg = kbeg + part * qlen;
+    kend = min(kend, wbeg + qlen);
+    lim = max(min(qr, kend - 1), -1);
+    if (lim < wbeg) lim = -1;
+    const int wmax = __builtin_amdgcn_readfirstlane(wave_max(lim));
+    t_beg = wbeg / T::BN;
+    t_end = wmax < wbeg ? t_beg : wmax / T::BN + 1;
+    t_step = 1;
+    // the first K tile, then Q, then the first V tile: one memory latency for all three. Loads return in issue
+    // order, so the explicit wait for K(t_beg) before the first S^T (at most the V tile's DW loads outstanding)
+    // also covers Q; the waits the compiler adds for Q, which does not count the tile loads, are only stricter.
+    if (t_end > t_beg) kplan.template tile<2>(kb_, Kb, p.ksM, kfast, t_beg * T::BN, kend, 0, lane);
+#pragma unroll
+    for (int ks = 0; ks < T::QK; ++ks)
+      qf[ks] = as_bf16x8(rvalid ? ld16(qrow + 16 * ks + 8 * hf) : u32x4_t{0u, 0u, 0u, 0u});
+    if (t_end > t_beg) vplan.template tile<2>(vb_, Vb, p.vsM, vfast, t_beg * T::BN, kend, 0, lane);
+  }
+  const int wmin = ROWS ? wave_ext_dpp<false>(lim) : __builtin_amdgcn_readfirstlane(wave_min(lim));
 
   f32x16_t o[T::DB];
 #pragma unroll
@@ -856,10 +900,9 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   f32x16_t s[T::NKB];
   uint32_t pk[T::NKB][8];
 
-  if (t_end > t_beg) vplan.template tile<2>(vb_, Vb, p.vsM, vfast, t_beg * T::BN, wend, 0, lane);
-  for (int t = t_beg; t < t_end; ++t) {
-    const int k0 = t * T::BN;
-    const bool more = t + 1 < t_end;
+  for (int t = t_beg; t < t_end; t += t_step) {
+    const int k0 = t * T::BN, kn = k0 + t_step * T::BN;  // this tile's first key, the next tile's
+    const bool more = t + t_step < t_end;
     __builtin_amdgcn_s_waitcnt(vmcnt_le(DW));  // K(t) landed (V(t) may be in flight)
 #pragma unroll
     for (int kb = 0; kb < T::NKB; ++kb) {
@@ -872,7 +915,7 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
       }
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the K tile has been read
-    if (more) kplan.template tile<2>(kb_, Kb, p.ksM, kfast, k0 + T::BN, wend, 0, lane);
+    if (more) kplan.template tile<LK>(kb_, Kb, p.ksM, kfast, kn, kend, 0, lane);
     if (k0 + T::BN - 1 > wmin) {
 #pragma unroll
       for (int kb = 0; kb < T::NKB; ++kb)
@@ -924,20 +967,24 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
       for (int db = 0; db < T::DB; ++db) o[db] = mfma32(v_operand<HD>(vb_, db, ss, vbase), pb, o[db]);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the V tile has been read
-    if (more) vplan.template tile<2>(vb_, Vb, p.vsM, vfast, k0 + T::BN, wend, 0, lane);
+    if (more) vplan.template tile<LK>(vb_, Vb, p.vsM, vfast, kn, kend, 0, lane);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
 
   // ---- merge the P partials of each split through LDS (the tile buffers are free once every wavefront is here)
   const float l = halves_sum(l_run);
   __syncthreads();
-  float* om = reinterpret_cast<float*>(&L);  // [DEC_NW][32 rows][HD]
+  // [DEC_NW][32 rows][HD], 16-byte groups of row x XOR-swizzled by x & 15: a wavefront's stores of 4 dims of its
+  // 32 rows, and the merge's reads along a row, spread over the banks (unswizzled, the rows' equal dims share a
+  // bank: 32-way conflicts, ~2 us per merge)
+  float* om = reinterpret_cast<float*>(&L);
+  auto omx = [](int x, int d) { return x * HD + (d ^ ((x & 15) << 2)); };
 #pragma unroll
   for (int db = 0; db < T::DB; ++db)
 #pragma unroll
     for (int q4 = 0; q4 < 4; ++q4) {
       const int d = 32 * db + 8 * q4 + 4 * hf;
-      *reinterpret_cast<f32x4_t*>(om + (w * 32 + lr) * HD + d) =
+      *reinterpret_cast<f32x4_t*>(om + omx(w * 32 + lr, d)) =
           f32x4_t{o[db][4 * q4 + 0], o[db][4 * q4 + 1], o[db][4 * q4 + 2], o[db][4 * q4 + 3]};
     }
   if (hf == 0) {
@@ -946,6 +993,56 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   }
   __syncthreads();
   if (!active) return;
+  if (ROWS) {
+    // final rows, 8 dims per thread: O = sum_w f_w O_w / sum_w f_w l_w with f_w = 2^(m_w - max_w m_w), and
+    // LSE = ln 2 * (max + log2 of the merged sum)
+    constexpr int U = HD / 8;
+    const int rows = min(32, p.M - rb * 32);
+    for (int u = tid; u < rows * U; u += 64 * DEC_NW) {
+      const int row = u / U, d0 = (u - row * U) * 8;
+      // every LDS read of the unit first (one round trip), then the arithmetic
+      float mw[DEC_NW], lw[DEC_NW];
+      f32x4_t a0[DEC_NW], a1[DEC_NW];
+#pragma unroll
+      for (int ww = 0; ww < DEC_NW; ++ww) {
+        mw[ww] = mm[ww * 32 + row];
+        lw[ww] = lm[ww * 32 + row];
+        a0[ww] = *reinterpret_cast<const f32x4_t*>(om + omx(ww * 32 + row, d0));
+        a1[ww] = *reinterpret_cast<const f32x4_t*>(om + omx(ww * 32 + row, d0 + 4));
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int ww = 0; ww < DEC_NW; ++ww) mx = fmaxf(mx, mw[ww]);
+      float lsum = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ww = 0; ww < DEC_NW; ++ww) {
+        const float f = mw[ww] == -INFINITY ? 0.f : fast_exp2(mw[ww] - mx);  // all -inf: every f is 0
+        lsum += f * lw[ww];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc[e] += f * a0[ww][e];
+          acc[4 + e] += f * a1[ww][e];
+        }
+      }
+      const int rr = rb * 32 + row, tq = rr / p.G, gq = rr - tq * p.G;
+      if (p.lse && d0 == 0)
+        p.lse[(long long)b * p.lsB + (long long)hk * p.lsH + (long long)tq * p.lsT + (long long)gq * p.lsG] =
+            lsum > 0.f ? (mx + log2f(lsum)) * 0.69314718055994530942f : -INFINITY;
+      if (!p.o) continue;
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      uint32_t pk8[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pk8[e] = pack_bf16x2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
+      uint16_t* orow = p.o + (long long)b * p.osB + (long long)hk * p.osH + (long long)tq * p.osT + (long long)gq * p.osG + d0;
+      if (o_vec8) {
+        *reinterpret_cast<u32x4_t*>(orow) = u32x4_t{pk8[0], pk8[1], pk8[2], pk8[3]};
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) reinterpret_cast<uint32_t*>(orow)[e] = pk8[e];
+      }
+    }
+    return;
+  }
   const int w0 = w - part;  // first wavefront of this split's group
   const long long prow0 = ((long long)(b * p.H + hk) * p.num_splits + split) * p.M;
   for (int idx = part * 64 + lane; idx < p.M * HD; idx += P * 64) {
@@ -958,7 +1055,7 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
         const float mw = mm[ww * 32 + row];
         const float f = mw == -INFINITY ? 0.f : fast_exp2(mw - mx);
         lsum += f * lm[ww * 32 + row];
-        acc += f * om[(ww * 32 + row) * HD + d];
+        acc += f * om[omx(ww * 32 + row, d)];
       }
     }
     p.ws_o[(prow0 + row) * HD + d] = lsum > 0.f ? acc / lsum : 0.f;
@@ -1160,9 +1257,28 @@ static int launch_fwd_pp(FwdParams p, hipStream_t stream) {
   return (int)hipGetLastError();
 }
 
+// The row-block form of the decode kernel (head_dim 128, qpos mode): one 4-wavefront workgroup per 32-row block.
+static int launch_fwd_rows(const FwdParams& p, hipStream_t stream) {
+  const long long nwg = (long long)p.B * p.H * ((p.M + 31) / 32);
+  if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
+  const int o_vec8 = p.o && aligned_elems(p.o, 8, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0;
+  hipLaunchKernelGGL((fmha_decode_kernel<128, false, true>), dim3((unsigned)nwg), dim3(64 * DEC_NW), 0, stream, p,
+                     DEC_NW, o_vec8);
+  return (int)hipGetLastError();
+}
+
 int launch_fwd(const FwdParams& p0, int head_dim, int mode, bool post, hipStream_t stream) {
   FwdParams p = p0;
   if (const int rc = prepare(p, post)) return rc;
+  // head_dim 128 qpos prefills whose 256-row items would occupy at most a quarter of the CUs (config 1: 16 items):
+  // 32-row blocks with their keys split over 4 wavefronts, 8 times the workgroups of the ping-pong kernel
+  if (head_dim == 128 && !post && !p.qpos0_block && mode == MODE_QPOS) {
+    const long long pp_items = (long long)p.B * p.H * (((long long)p.M + PP_BM - 1) / PP_BM);
+    if (pp_items > 0) {
+      const int cus = device_cus(stream);
+      if (cus > 0 && pp_items * 4 <= cus) return launch_fwd_rows(p, stream);
+    }
+  }
   // head_dim 128 qpos / varlen without the POST epilogue: the ping-pong kernel once a row tile has enough rows
   // to fill both groups (short query blocks, e.g. decode, keep the 4-wavefront kernel); the drop-in block rule
   // (qpos0_block) lives in the 4-wavefront kernel only
@@ -1241,11 +1357,11 @@ int launch_decode_split(FwdParams p, int head_dim, int P, bool post, hipStream_t
   if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
   if (head_dim == 128) {
     if (post || p.qpos0_block) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL((fmha_decode_kernel<128, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
+    hipLaunchKernelGGL((fmha_decode_kernel<128, false, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P, 0);
   } else if (p.qpos0_block) {
-    hipLaunchKernelGGL((fmha_decode_kernel<256, true>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
+    hipLaunchKernelGGL((fmha_decode_kernel<256, true, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P, 0);
   } else {
-    hipLaunchKernelGGL((fmha_decode_kernel<256, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
+    hipLaunchKernelGGL((fmha_decode_kernel<256, false, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P, 0);
   }
   if (const int rc = (int)hipGetLastError()) return rc;
   return launch_combine(p, head_dim, post, stream);

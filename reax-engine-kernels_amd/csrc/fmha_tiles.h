@@ -1,6 +1,8 @@
 // Shared building blocks of the gfx950 attention kernels: K/V tile geometry, the LDS swizzle, direct-to-LDS tile
 // loads, MFMA operand addressing and the wavefront reductions.
 #pragma once
+#include <climits>
+
 #include "fmha_common.h"
 
 namespace reax {
@@ -216,6 +218,25 @@ __device__ __forceinline__ int wave_min(int x) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) x = min(x, __shfl_xor(x, off, 64));
   return x;
+}
+
+// The same as a scalar, with DPP steps instead of six ds_bpermute round trips (all 64 lanes must be active):
+// quad permutes [1,0,3,2] and [2,3,0,1] give each quad its extremum, row shifts by 4 and 8 carry it to lane 15 of
+// each 16-lane row, and the row broadcasts of lane 15 (into rows 1 and 3) and lane 31 (into rows 2 and 3) leave
+// the wavefront's extremum in lane 63, read back as a scalar. Lanes whose DPP source lies outside the row, or
+// whose row is masked off, take the identity. (Used where a kernel's prologue waits on it; inside the larger
+// kernels the DPP form raised register pressure into scratch spills.)
+template <bool MAX>
+__device__ __forceinline__ int wave_ext_dpp(int x) {
+  constexpr int ID = MAX ? INT_MIN : INT_MAX;
+  auto op = [](int a, int b) { return MAX ? max(a, b) : min(a, b); };
+  x = op(x, __builtin_amdgcn_update_dpp(ID, x, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  x = op(x, __builtin_amdgcn_update_dpp(ID, x, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  x = op(x, __builtin_amdgcn_update_dpp(ID, x, 0x114, 0xF, 0xF, false));  // row_shr:4
+  x = op(x, __builtin_amdgcn_update_dpp(ID, x, 0x118, 0xF, 0xF, false));  // row_shr:8
+  x = op(x, __builtin_amdgcn_update_dpp(ID, x, 0x142, 0xA, 0xF, false));  // row_bcast:15
+  x = op(x, __builtin_amdgcn_update_dpp(ID, x, 0x143, 0xC, 0xF, false));  // row_bcast:31
+  return __builtin_amdgcn_readlane(x, 63);
 }
 
 // Lazy rescaling: the running max (log2 units) is raised only when a tile's max exceeds it by more than

@@ -113,12 +113,26 @@ SMALL = [
     FC.Case("d256_s300_g2", B=1, S=300, N=300, Hq=4, Hkv=2, D=256, mode="causal", seed=7),
     FC.Case("d256_full_n129", B=2, S=17, N=129, Hq=2, Hkv=1, D=256, mode="full", seed=8),
     FC.Case("n1_single_key", B=1, S=5, N=1, Hq=4, Hkv=2, D=128, mode="full", seed=9),
+    # enough (b, KV head) row tiles for the ping-pong kernel (the shapes above take the row-block kernel)
+    FC.Case("pp_ragged_s77_b9", B=9, S=77, N=77, Hq=32, Hkv=8, D=128, mode="causal", seed=10),
+    FC.Case("pp_prefix_s50_n333", B=9, S=50, N=333, Hq=32, Hkv=8, D=128, mode="causal", seed=11),
 ]
+
+
+def qx_route(c: FC.Case) -> str:
+    """The head_dim-128 qx kernel a shape reaches: the row-block kernel when the ping-pong kernel's 256-row items
+    would occupy at most a quarter of the CUs, else the ping-pong kernel (more than 64 folded rows) or the
+    4-wavefront kernel."""
+    M = c.S * c.G
+    items = c.B * c.Hkv * -(-M // 256)
+    if c.D == 128 and items * 4 <= torch.cuda.get_device_properties(0).multi_processor_count:
+        return "rows"
+    return "pp" if M > 64 else "fwd4"
 
 
 @pytest.mark.parametrize("c", SMALL, ids=lambda c: c.name)
 def test_qx_against_oracle(c):
-    _say(f"qx {c.name} B{c.B} S{c.S} N{c.N} Hq{c.Hq} Hkv{c.Hkv} D{c.D}")
+    _say(f"qx {c.name} B{c.B} S{c.S} N{c.N} Hq{c.Hq} Hkv{c.Hkv} D{c.D} ({qx_route(c)} kernel)")
     a = FC.build(c)
     og, lg = run_qx(c, a)
     o, lse = FC.oracle_ref(c, a)
@@ -126,24 +140,27 @@ def test_qx_against_oracle(c):
     _say(f"  {res}")
 
 
-def test_qx_qpos_edges():
-    """qpos < 0 rows give 0 / -inf; qpos = 0 rows reproduce V[0] exactly; qpos >= N sees every key."""
+@pytest.mark.parametrize("B,Hq,Hkv,route", [(1, 8, 2, "rows"), (9, 32, 8, "pp")], ids=["rows", "pp"])
+def test_qx_qpos_edges(B, Hq, Hkv, route):
+    """qpos < 0 rows give 0 / -inf; qpos = 0 rows reproduce V[0] exactly; qpos >= N sees every key; rows in any
+    order (qpos not increasing), on both head_dim-128 prefill kernels."""
     S, N = 40, 150
     rng = np.random.default_rng(21)
-    qp = rng.integers(-2, N + 4, size=(1, S)).astype(np.int32)
-    qp[0, :4] = [0, -1, N + 3, 63]
-    c = FC.Case("qpos_edges", B=1, S=S, N=N, Hq=8, Hkv=2, D=128, mode="qpos", seed=22, qpos=qp)
-    _say("qx qpos_edges")
+    qp = rng.integers(-2, N + 4, size=(B, S)).astype(np.int32)
+    qp[:, :4] = [0, -1, N + 3, 63]
+    c = FC.Case(f"qpos_edges_{route}", B=B, S=S, N=N, Hq=Hq, Hkv=Hkv, D=128, mode="qpos", seed=22, qpos=qp)
+    assert qx_route(c) == route
+    _say(f"qx {c.name}")
     a = FC.build(c)
     og, lg = run_qx(c, a)
     o, lse = FC.oracle_ref(c, a)
     FC.check_tolerance(og, o, lg, lse, where=c.name)
-    dead = qp[0] < 0
-    assert (og[0, dead] == 0).all() and np.isneginf(lg[0][:, dead]).all()
-    zero = np.nonzero(qp[0] == 0)[0]
-    for m in zero:
-        for hq in range(c.Hq):
-            assert (og[0, m, hq] == a["v"][0, 0, hq // c.G]).all(), "qpos = 0 must write V[0] exactly"
+    for b in range(B):
+        dead = qp[b] < 0
+        assert (og[b, dead] == 0).all() and np.isneginf(lg[b][:, dead]).all()
+        for m in np.nonzero(qp[b] == 0)[0]:
+            for hq in range(c.Hq):
+                assert (og[b, m, hq] == a["v"][b, 0, hq // c.G]).all(), "qpos = 0 must write V[0] exactly"
 
 
 # The head_dim-128 prefill kernel is persistent (one workgroup per CU, items in snake order, an XCD-aware split
@@ -163,12 +180,15 @@ def test_qx_persistent_multi_item(B, S, Hq, Hkv):
 # The head_dim-128 prefill kernel picks its output store by the output's alignment: rows 16-byte aligned go out as
 # whole rows staged through LDS, 8-byte aligned ones as 8-byte pieces, the rest as 4-byte pieces. An output view
 # into rows padded by `pad` elements selects each; the padding must stay untouched.
+# The row-block kernel stores 16 bytes per thread when the output's rows are 16-byte aligned, else 4-byte pieces.
 @pytest.mark.parametrize("pad", [8, 4, 2], ids=["rows16", "rows8", "rows4"])
-def test_qx_output_strides(pad):
+@pytest.mark.parametrize("B,Hq,Hkv,route", [(2, 8, 2, "rows"), (9, 32, 8, "pp")], ids=["rows", "pp"])
+def test_qx_output_strides(pad, B, Hq, Hkv, route):
     from reax_fmha import ops
 
-    c = FC.Case(f"ostride_pad{pad}", B=2, S=120, N=120, Hq=8, Hkv=2, D=128, mode="causal", seed=41 + pad)
-    _say(f"qx output rows padded by {pad}")
+    c = FC.Case(f"ostride_pad{pad}_{route}", B=B, S=120, N=120, Hq=Hq, Hkv=Hkv, D=128, mode="causal", seed=41 + pad)
+    assert qx_route(c) == route
+    _say(f"qx output rows padded by {pad} ({route} kernel)")
     a = FC.build(c)
     q, k, v = dev(a["q"]), dev(a["k"]), dev(a["v"])
     qpos = torch.from_numpy(a["qpos"]).cuda()
@@ -179,6 +199,49 @@ def test_qx_output_strides(pad):
     assert (buf[..., c.D:] == -7.0).all(), "padding written"
     o_ref, lse_ref = FC.oracle_ref(c, a)
     FC.check_tolerance(host(o.contiguous()), o_ref, lse.cpu().numpy(), lse_ref, where=c.name)
+
+
+# The row-block kernel (head_dim-128 prefills too small to fill the GPU with 256-row items): 32-row blocks, the
+# block's keys cut into 4 runs of 64-key tiles, one per wavefront, merged in LDS. Partial last blocks, fewer rows
+# than a block, G = 1 and 16, key ranges of one tile to 65 (a partial last tile), runs left empty (a block seeing
+# fewer tiles than there are wavefronts), random qpos with negatives and qpos >= N, and no LSE output.
+ROWS = [
+    FC.Case("rows_ragged_b3_s77", B=3, S=77, N=77, Hq=8, Hkv=2, D=128, mode="causal", seed=51),
+    FC.Case("rows_m24_n4100", B=2, S=3, N=4100, Hq=16, Hkv=2, D=128, mode="full", seed=52),
+    FC.Case("rows_g1_s33_n600", B=1, S=33, N=600, Hq=4, Hkv=4, D=128, mode="causal", seed=53),
+    FC.Case("rows_g16_s130", B=1, S=130, N=130, Hq=16, Hkv=1, D=128, mode="causal", seed=54),
+    FC.Case("rows_qpos_rand", B=2, S=61, N=300, Hq=8, Hkv=2, D=128, mode="qpos", seed=55,
+            qpos=np.random.default_rng(56).integers(-3, 306, size=(2, 61)).astype(np.int32)),
+    FC.Case("rows_n65", B=1, S=9, N=65, Hq=8, Hkv=8, D=128, mode="full", seed=57),
+]
+
+
+@pytest.mark.parametrize("c", ROWS, ids=lambda c: c.name)
+@pytest.mark.parametrize("want_lse", [True, False], ids=["lse", "no_lse"])
+def test_qx_rows_kernel(c, want_lse):
+    assert qx_route(c) == "rows"
+    _say(f"qx rows {c.name} B{c.B} S{c.S} N{c.N} Hq{c.Hq} Hkv{c.Hkv} lse={want_lse}")
+    a = FC.build(c)
+    og, lg = run_qx(c, a, want_lse=want_lse)
+    o, lse = FC.oracle_ref(c, a)
+    res = FC.check_tolerance(og, o, lg, lse if want_lse else None, where=c.name)
+    _say(f"  {res}")
+
+
+# The routing bound: 64 ping-pong items on 256 CUs (a quarter) take the row-block kernel (512 workgroups, two per
+# CU in turn), 72 take the ping-pong kernel; both checked on a seeded token subset.
+@pytest.mark.parametrize("S,route", [(512, "rows"), (520, "pp")], ids=["rows_64_items", "pp_72_items"])
+def test_qx_route_bound(S, route):
+    c = FC.Case(f"route_s{S}", B=1, S=S, N=S, Hq=32, Hkv=8, D=128, mode="causal", seed=60 + S)
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the bound is placed for 256 CUs")
+    assert qx_route(c) == route
+    _say(f"qx {c.name} ({route} kernel)")
+    a = FC.build(c)
+    og, lg = run_qx(c, a)
+    toks = token_subset(S, 40, 61, edge=24)
+    o, lse = oracle_on_tokens(c, a, toks)
+    FC.check_tolerance(og[:, toks], o, lg[:, :, toks], lse, where=c.name)
 
 
 GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
