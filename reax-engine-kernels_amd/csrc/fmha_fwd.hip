@@ -777,8 +777,9 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
 // largest raw qpos among them is 0, every live row sees key 0 only, reax_fmha_v8.cu:155-162, 224-235).
 // ROWS: a prefill too small to fill the GPU with 256-row items (reax_fmha_qx at S 512: 16 items for 256 CUs).
 // The task is then a 32-row block (b, block, KV head) of any p.M, blocks with the most keys first; the workgroup's
-// 4 wavefronts cut the block's key range [0, its largest key limit] into 4 runs of whole tiles, and the merge
-// through LDS writes the final O (bf16, 16-byte stores when o_vec8) and LSE instead of split partials.
+// 4 wavefronts take tiles w, w + 4, ... of the block's key range [0, its largest key limit], and the merge through
+// LDS writes the final O (bf16; 8-byte pieces when o_vec8, i.e. rows 8-byte aligned) and LSE instead of split
+// partials.
 constexpr int DEC_NW = 4;
 
 template <int HD>
@@ -814,7 +815,7 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   const long long tk = active ? task : 0;
   const int hk = ROWS ? (int)((unsigned)tk % (unsigned)p.H) : (int)(tk % p.H);
   int split = 0, rb = 0, b = 0;
-  if (ROWS) {
+  if constexpr (ROWS) {
     const unsigned t32 = (unsigned)tk, bh = (unsigned)p.B * (unsigned)p.H;  // tk < B * nrb * H <= INT_MAX
     b = (int)((t32 / (unsigned)p.H) % (unsigned)p.B);
     rb = nrb - 1 - (int)(t32 / bh);
@@ -844,7 +845,7 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   bf16x8_t qf[T::QK];
   // tiles t_beg, t_beg + t_step, ... below t_end; keys above a row's lim are masked; tile loads stop at kend
   int t_beg, t_end, t_step, kend, lim;
-  if (ROWS) {
+  if constexpr (ROWS) {
     // tiles part, part + P, ...: the first one does not depend on qpos, so Q, then its K and V, then qpos go out
     // together (one memory latency; a block seeing fewer tiles leaves the tile unused). Loads complete in issue
     // order: the wait the compiler puts before qpos's use covers Q and the tile too, and its wait for Q before
@@ -933,12 +934,16 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
     mx = halves_max(mx) * cc;
     if (__any(mx > m_run + RESCALE_SLACK)) {
       const float m_new = fmaxf(m_run, mx);
-      const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
-      l_run *= alpha;
+      // before the wavefront's first admitted key every row's O and sum are still 0: nothing to rescale (with
+      // one or two tiles per wavefront, the 64 accumulator multiplies are a visible part of the loop)
+      if (__any(m_run != -INFINITY)) {
+        const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+        l_run *= alpha;
 #pragma unroll
-      for (int db = 0; db < T::DB; ++db)
+        for (int db = 0; db < T::DB; ++db)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+          for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+      }
       m_run = m_new;
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
@@ -971,8 +976,87 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
 
-  // ---- merge the P partials of each split through LDS (the tile buffers are free once every wavefront is here)
   const float l = halves_sum(l_run);
+  if constexpr (ROWS) {
+    // ---- merge of a row block, wavefront w finalising dim block w (HD = 128: 4 blocks of 32 dims). Row maxima
+    // and sums meet in LDS first; every lane (one row) then weights its own partial by
+    //   g_w = 2^(m_w - M) / L,   M = max_w m_w,   L = sum_w 2^(m_w - M) l_w,
+    // so the final O is the plain sum of the weighted partials: each wavefront writes the three dim blocks the
+    // others finalise (48 KB in all, against 64 KB written and read back with the weights applied per element),
+    // reads its own block's three partials and adds its registers. LSE = ln 2 (M + log2 L).
+    static_assert(T::DB == DEC_NW, "one 32-dim block per wavefront");
+    if (hf == 0) {
+      mm[w * 32 + lr] = l > 0.f ? m_run : -INFINITY;
+      lm[w * 32 + lr] = l;
+    }
+    __syncthreads();  // the tile buffers are free, the maxima and sums visible
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < DEC_NW; ++ww) M = fmaxf(M, mm[ww * 32 + lr]);
+    float Lsum = 0.f, gself = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < DEC_NW; ++ww) {
+      const float mw = mm[ww * 32 + lr];
+      const float f = mw == -INFINITY ? 0.f : fast_exp2(mw - M);  // every row maximum -inf: all f are 0
+      Lsum += f * lm[ww * 32 + lr];
+      if (ww == w) gself = f;
+    }
+    const float wt = Lsum > 0.f ? gself / Lsum : 0.f;  // this wavefront's weight g_w
+    // [dim block][source wavefront][32 rows][32 dims] fp32 (64 KB); the 4-dim groups of row x XOR-swizzled by
+    // (x >> 1) & 7 (rows are 128 bytes: rows x and x + 1 cover the two bank halves, the XOR spreads 8 row pairs
+    // over the groups, so a wavefront's 16-byte stores and loads of 16 rows hit 16 distinct bank groups)
+    float* om = reinterpret_cast<float*>(&L);
+    auto oix = [](int db, int src, int x, int grp) {
+      return ((db * DEC_NW + src) * 32 + x) * 32 + ((grp ^ ((x >> 1) & 7)) << 2);
+    };
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db) {
+      if (db == w) continue;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<f32x4_t*>(om + oix(db, w, lr, 2 * q4 + hf)) =
+            f32x4_t{o[db][4 * q4 + 0] * wt, o[db][4 * q4 + 1] * wt, o[db][4 * q4 + 2] * wt, o[db][4 * q4 + 3] * wt};
+    }
+    __syncthreads();
+    f32x16_t fin;
+#pragma unroll
+    for (int db = 0; db < T::DB; ++db)
+      if (db == w)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) fin[e] = o[db][e] * wt;
+#pragma unroll
+    for (int src = 0; src < DEC_NW; ++src) {
+      if (src == w) continue;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(om + oix(w, src, lr, 2 * q4 + hf));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) fin[4 * q4 + e] += a[e];
+      }
+    }
+    if (!rvalid) return;
+    if (p.lse && w == 0 && hf == 0)
+      p.lse[(long long)b * p.lsB + (long long)hk * p.lsH + (long long)tok * p.lsT + (long long)g * p.lsG] =
+          Lsum > 0.f ? (M + log2f(Lsum)) * 0.69314718055994530942f : -INFINITY;
+    if (!p.o) return;
+    // row r, dims 32 w + 8 q4 + 4 hf .. + 3: one 8-byte piece per q4 (two 4-byte pieces when rows are only
+    // 4-byte aligned)
+    uint16_t* orow = p.o + (long long)b * p.osB + (long long)hk * p.osH + (long long)tok * p.osT +
+                     (long long)g * p.osG + 32 * w + 4 * hf;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const uint32_t w0 = pack_bf16x2(fin[4 * q4 + 0], fin[4 * q4 + 1]);
+      const uint32_t w1 = pack_bf16x2(fin[4 * q4 + 2], fin[4 * q4 + 3]);
+      if (o_vec8) {
+        *reinterpret_cast<u32x2_t*>(orow + 8 * q4) = u32x2_t{w0, w1};
+      } else {
+        reinterpret_cast<uint32_t*>(orow + 8 * q4)[0] = w0;
+        reinterpret_cast<uint32_t*>(orow + 8 * q4)[1] = w1;
+      }
+    }
+    return;
+  }
+  // ---- merge the P partials of each split through LDS (the tile buffers are free once every wavefront is here)
   __syncthreads();
   // [DEC_NW][32 rows][HD], 16-byte groups of row x XOR-swizzled by x & 15: a wavefront's stores of 4 dims of its
   // 32 rows, and the merge's reads along a row, spread over the banks (unswizzled, the rows' equal dims share a
@@ -993,56 +1077,6 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   }
   __syncthreads();
   if (!active) return;
-  if (ROWS) {
-    // final rows, 8 dims per thread: O = sum_w f_w O_w / sum_w f_w l_w with f_w = 2^(m_w - max_w m_w), and
-    // LSE = ln 2 * (max + log2 of the merged sum)
-    constexpr int U = HD / 8;
-    const int rows = min(32, p.M - rb * 32);
-    for (int u = tid; u < rows * U; u += 64 * DEC_NW) {
-      const int row = u / U, d0 = (u - row * U) * 8;
-      // every LDS read of the unit first (one round trip), then the arithmetic
-      float mw[DEC_NW], lw[DEC_NW];
-      f32x4_t a0[DEC_NW], a1[DEC_NW];
-#pragma unroll
-      for (int ww = 0; ww < DEC_NW; ++ww) {
-        mw[ww] = mm[ww * 32 + row];
-        lw[ww] = lm[ww * 32 + row];
-        a0[ww] = *reinterpret_cast<const f32x4_t*>(om + omx(ww * 32 + row, d0));
-        a1[ww] = *reinterpret_cast<const f32x4_t*>(om + omx(ww * 32 + row, d0 + 4));
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int ww = 0; ww < DEC_NW; ++ww) mx = fmaxf(mx, mw[ww]);
-      float lsum = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ww = 0; ww < DEC_NW; ++ww) {
-        const float f = mw[ww] == -INFINITY ? 0.f : fast_exp2(mw[ww] - mx);  // all -inf: every f is 0
-        lsum += f * lw[ww];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          acc[e] += f * a0[ww][e];
-          acc[4 + e] += f * a1[ww][e];
-        }
-      }
-      const int rr = rb * 32 + row, tq = rr / p.G, gq = rr - tq * p.G;
-      if (p.lse && d0 == 0)
-        p.lse[(long long)b * p.lsB + (long long)hk * p.lsH + (long long)tq * p.lsT + (long long)gq * p.lsG] =
-            lsum > 0.f ? (mx + log2f(lsum)) * 0.69314718055994530942f : -INFINITY;
-      if (!p.o) continue;
-      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-      uint32_t pk8[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pk8[e] = pack_bf16x2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
-      uint16_t* orow = p.o + (long long)b * p.osB + (long long)hk * p.osH + (long long)tq * p.osT + (long long)gq * p.osG + d0;
-      if (o_vec8) {
-        *reinterpret_cast<u32x4_t*>(orow) = u32x4_t{pk8[0], pk8[1], pk8[2], pk8[3]};
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) reinterpret_cast<uint32_t*>(orow)[e] = pk8[e];
-      }
-    }
-    return;
-  }
   const int w0 = w - part;  // first wavefront of this split's group
   const long long prow0 = ((long long)(b * p.H + hk) * p.num_splits + split) * p.M;
   for (int idx = part * 64 + lane; idx < p.M * HD; idx += P * 64) {
@@ -1261,7 +1295,7 @@ static int launch_fwd_pp(FwdParams p, hipStream_t stream) {
 static int launch_fwd_rows(const FwdParams& p, hipStream_t stream) {
   const long long nwg = (long long)p.B * p.H * ((p.M + 31) / 32);
   if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
-  const int o_vec8 = p.o && aligned_elems(p.o, 8, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0;
+  const int o_vec8 = p.o && aligned_elems(p.o, 4, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0;  // 8-byte output pieces
   hipLaunchKernelGGL((fmha_decode_kernel<128, false, true>), dim3((unsigned)nwg), dim3(64 * DEC_NW), 0, stream, p,
                      DEC_NW, o_vec8);
   return (int)hipGetLastError();
