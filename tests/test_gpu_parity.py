@@ -116,18 +116,21 @@ SMALL = [
     # enough (b, KV head) row tiles for the ping-pong kernel (the shapes above take the row-block kernel)
     FC.Case("pp_ragged_s77_b9", B=9, S=77, N=77, Hq=32, Hkv=8, D=128, mode="causal", seed=10),
     FC.Case("pp_prefix_s50_n333", B=9, S=50, N=333, Hq=32, Hkv=8, D=128, mode="causal", seed=11),
+    # at most 128 folded rows with too many (b, KV head) pairs for the row-block kernel: the 4-wavefront kernel
+    FC.Case("fwd4_s20_b9", B=9, S=20, N=20, Hq=32, Hkv=8, D=128, mode="causal", seed=12),
+    FC.Case("fwd4_s5_n700_b9", B=9, S=5, N=700, Hq=32, Hkv=8, D=128, mode="causal", seed=13),
 ]
 
 
 def qx_route(c: FC.Case) -> str:
     """The head_dim-128 qx kernel a shape reaches: the row-block kernel when the ping-pong kernel's 256-row items
-    would occupy at most a quarter of the CUs, else the ping-pong kernel (more than 64 folded rows) or the
-    4-wavefront kernel."""
+    would occupy at most a quarter of the CUs, else the ping-pong kernel (more than 128 folded rows) or the
+    4-wavefront kernel (128 rows a workgroup)."""
     M = c.S * c.G
     items = c.B * c.Hkv * -(-M // 256)
     if c.D == 128 and items * 4 <= torch.cuda.get_device_properties(0).multi_processor_count:
         return "rows"
-    return "pp" if M > 64 else "fwd4"
+    return "pp" if M > 128 else "fwd4"
 
 
 @pytest.mark.parametrize("c", SMALL, ids=lambda c: c.name)
@@ -470,7 +473,8 @@ def run_varlen(c, a, want_lse=True):
     return host(o), (lse.cpu().numpy() if lse is not None else None)
 
 
-@pytest.mark.parametrize("seqlens,D", [([5, 300, 0, 1, 129, 64], 128), ([200, 33, 97], 256)])
+# the third case keeps max_seqlen * G <= 128 (head_dim 128): the 4-wavefront kernel instead of the ping-pong one
+@pytest.mark.parametrize("seqlens,D", [([5, 300, 0, 1, 129, 64], 128), ([200, 33, 97], 256), ([5, 30, 0, 1, 17, 32], 128)])
 def test_varlen_ragged(seqlens, D):
     c = FC.Case("varlen", B=1, S=0, N=0, Hq=8, Hkv=2, D=D, mode="varlen", seed=71, seqlens=seqlens)
     _say(f"varlen {seqlens} D{D}")
