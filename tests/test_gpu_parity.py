@@ -247,6 +247,37 @@ def test_qx_route_bound(S, route):
     FC.check_tolerance(og[:, toks], o, lg[:, :, toks], lse, where=c.name)
 
 
+def _random_rows_cases(n, seed):
+    """Seeded random shapes for the row-block kernel: B 1-3, Hkv 1-4, G 1/2/4/8/16, S 1-300 tokens, N 1-1200 keys,
+    causal, full or random qpos (negatives and qpos >= N included), each kept within the row-block bound
+    (B * Hkv * ceil(S * G / 256) <= 64) and small enough for the double-precision oracle."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        B, Hkv, G = int(rng.integers(1, 4)), int(rng.integers(1, 5)), int(rng.choice([1, 2, 4, 8, 16]))
+        S, N = int(rng.integers(1, 301)), int(rng.integers(1, 1201))
+        if B * Hkv * -(-S * G // 256) > 64 or B * S * Hkv * G * N > 6_000_000:
+            continue
+        mode = str(rng.choice(["causal", "full", "qpos"]))
+        if mode == "causal" and N < S:
+            N = S
+        qp = rng.integers(-3, N + 3, size=(B, S)).astype(np.int32) if mode == "qpos" else None
+        out.append(FC.Case(f"rand{len(out)}_b{B}_h{Hkv}_g{G}_s{S}_n{N}_{mode}", B=B, S=S, N=N, Hq=Hkv * G, Hkv=Hkv,
+                           D=128, mode=mode, seed=int(rng.integers(1 << 30)), qpos=qp))
+    return out
+
+
+# Random shapes through the row-block kernel against the oracle (a sweep on top of the hand-picked cases above).
+@pytest.mark.parametrize("c", _random_rows_cases(24, 2026), ids=lambda c: c.name)
+def test_qx_rows_random(c):
+    assert qx_route(c) == "rows"
+    _say(f"qx rows random {c.name}")
+    a = FC.build(c)
+    og, lg = run_qx(c, a)
+    o, lse = FC.oracle_ref(c, a)
+    FC.check_tolerance(og, o, lg, lse, where=c.name)
+
+
 GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
 
 
