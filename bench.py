@@ -655,8 +655,7 @@ def main():
         "c5": (lambda: prep_post(torch, ops, W.CONFIGS[5]), W.CONFIGS[5],
                "reax_fmha_qp (libreax_fmha_post.so): drop-in ABI, sigmoid gate epilogue"),
     }
-    traffic = {"c1": None, "c3": os.path.join(PROFILES, "fmha_fwd_c3_pmc.txt"),
-               "c5": os.path.join(PROFILES, "fmha_fwd_c5_pmc.txt")}
+    traffic = {c: os.path.join(PROFILES, "fmha_fwd_%s_pmc.txt" % c) for c in ("c1", "c3", "c5")}
     if one in preps:
         mk, cfg, entry = preps[one]
         ms = float(np.median(time_launches(torch, mk(), args.warmup, args.iters)))
