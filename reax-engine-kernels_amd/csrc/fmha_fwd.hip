@@ -470,10 +470,9 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   const uint32_t vbase = v_lane_base<HD>(lane);
 
   // softmax of tile t: S in s[] -> P in pk[] (bf16), running max / row sum, lazy O rescale
-  auto softmax = [&](int t) __attribute__((always_inline)) {
-    const int k0 = t * T::BN;
-    if (k0 > wmax) return;
-    if (k0 + T::BN - 1 > wmin) {
+  // softmax_core<MASK>: MASK = false only where the caller knows that every row of the wavefront sees the whole tile
+  auto softmax_core = [&](auto maskc, int k0) __attribute__((always_inline)) {
+    if (decltype(maskc)::value && k0 + T::BN - 1 > wmin) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -523,6 +522,11 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
         pk[kb][i] = pack_bf16x2(s[kb][2 * i], s[kb][2 * i + 1]);
       }
     l_run += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+  };
+  auto softmax = [&](int t) __attribute__((always_inline)) {
+    const int k0 = t * T::BN;
+    if (k0 > wmax) return;
+    softmax_core(std::true_type{}, k0);
   };
   // MFMA phase of step t: O += V(t-1)^T P(t-1)^T (if PV), then S(t) = K(t) Q^T (if QK), one slot per MFMA in a
   // fixed order (scheduling barriers between slots): each LDS operand read goes out D = 4 MFMAs ahead of its
@@ -646,11 +650,74 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
       }
       __syncthreads();
     };
-    for (int t = 0; t <= t_end; t += NS) {
+    // Steady state: steps 1 <= t <= t_fast in which both MFMA halves run, no row of this wavefront needs the mask
+    // pass on tile t - 1 or t, and group 0's two loads are whole tiles with 32-bit row offsets. They run as pairs
+    // (odd t, then even) of a straight-line body: buffers fixed at compile time, the load sources advanced by one
+    // tile per step, no per-step flags. t_fast is per wavefront; every step, fast or not, has the same two
+    // barriers, so the wavefronts stay in step.
+    int t_fast = 0;
+    if (MODE != MODE_VARLEN && kfast && vfast) {
+      const int lm = min(wmin, wmax);  // wmax < 0: no row of the wavefront sees a key
+      t_fast = min(min(t_end - 2, Nb / T::BN - 2), lm >= T::BN - 1 ? (lm + 1) / T::BN - 1 : 0);
+    }
+    auto fast_step = [&](auto jc, int t, const uint8_t* ksrc, const uint8_t* vsrc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+      const uint8_t* kb_t = kring[j];
+      uint8_t* kb_fill = kring[j ^ 1];
+      const uint8_t* vb_prev = vring[j ^ 1];
+      uint8_t* vb_fill = vring[j];
+      constexpr int DW4 = Dma<HD, PP_NW / 2>::DW;
+      auto dma = [&](int jj) __attribute__((always_inline)) {
+        const bool isk = jj < DW4;
+        const int i = isk ? jj : jj - DW4;
+        uint32_t o = isk ? kplan.off[i] : vplan.off[i];
+        asm volatile("" : "+v"(o));
+        const uint8_t* src = (isk ? ksrc : vsrc) + o;
+        const uint32_t m0 = (uint32_t)reinterpret_cast<uintptr_t>(isk ? kb_fill : vb_fill) + (wu * DW4 + i) * 1024;
+        asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+      };
+      auto no_dma = [](int) {};
+      using Y = std::true_type;
+      using N = std::false_type;
+      if (grp == 0)
+        mfma_block(Y{}, Y{}, kb_t, vb_prev, dma);
+      else
+        softmax_core(N{}, (t - 1) * T::BN);
+      exec_barrier();
+      if (grp == 0)
+        softmax_core(N{}, t * T::BN);
+      else
+        mfma_block(Y{}, Y{}, kb_t, vb_prev, no_dma);
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+    };
+    static_assert(NS == 2, "the fast steps alternate two K/V buffers");
+    // step t loads K(t+1) and V(t)
+    auto ksrc_of = [&](int t) __attribute__((always_inline)) {
+      return reinterpret_cast<const uint8_t*>(Kb + (long long)(t + 1) * T::BN * p.ksM);
+    };
+    auto vsrc_of = [&](int t) __attribute__((always_inline)) {
+      return reinterpret_cast<const uint8_t*>(Vb + (long long)t * T::BN * p.vsM);
+    };
+    if constexpr (MODE == MODE_VARLEN) {
+      for (int t = 0; t <= t_end; t += NS) {
 #pragma unroll
-      for (int j = 0; j < NS; ++j)
-        if (t + j <= t_end)
-          step(t + j, kring[j], kring[(j + NS - 1) % NS], vring[(j + NS - 1) % NS], vring[(j + NS - 2) % NS]);
+        for (int j = 0; j < NS; ++j)
+          if (t + j <= t_end)
+            step(t + j, kring[j], kring[(j + NS - 1) % NS], vring[(j + NS - 1) % NS], vring[(j + NS - 2) % NS]);
+      }
+    } else {
+    // step 0 (K(0) only), then pairs (odd t, t + 1)
+    step(0, kring[0], kring[1], vring[1], vring[0]);
+    for (int t = 1; t <= t_end; t += NS) {
+      if (t + 1 <= t_fast) {
+        fast_step(std::integral_constant<int, 1>{}, t, ksrc_of(t), vsrc_of(t));
+        fast_step(std::integral_constant<int, 0>{}, t + 1, ksrc_of(t + 1), vsrc_of(t + 1));
+        continue;
+      }
+      step(t, kring[1], kring[0], vring[0], vring[1]);
+      if (t + 1 <= t_end) step(t + 1, kring[0], kring[1], vring[1], vring[0]);
+    }
     }
   }
 
