@@ -79,7 +79,7 @@ def mfma_entry(cfg, ms, entry, traffic_path=None, extra=None):
     """A config's bench object: TFLOP/s of its admitted-pair FLOPs at `ms` per launch, with the roofline against
     the dense bf16 MFMA peak."""
     tf = cfg.flops() / (ms * 1e-3) / 1e12
-    e = {"workload": cfg.name, "value": round(tf, 2), "unit": "TFLOP/s", "ms": round(ms, 4),
+    e = {"workload": cfg.name, "value": round(tf, 2), "unit": "TFLOP/s", "ms": round(ms, 6),
          "flops": cfg.flops(), "entry_point": entry,
          "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": W.BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                       "frac": round(tf / W.BF16_PEAK_TFLOPS, 4),
@@ -685,10 +685,14 @@ def main():
             legs[f"qp_decode_b{B}"] = bench_qp_decode(torch, ops, qcfg, 20)
             torch.cuda.empty_cache()
     if not args.no_configs:
+        # untimed launches first, then the median of the timed ones: the short configs get more of both (config 1's
+        # launch is ~10 us: 300 warm launches are 3 ms, in which the clock settles as it does for the others)
+        warm_iters = {"c1": (300, max(args.iters, 100)), "c3": (100, max(args.iters, 50)), "c5": (3, args.iters)}
         for name in ("c1", "c3", "c5"):
             mk, ccfg, entry = preps[name]
             run = mk()
-            ms = float(np.median(time_launches(torch, run, 10, args.iters)))
+            warm, iters = warm_iters[name]
+            ms = float(np.median(time_launches(torch, run, warm, iters)))
             del run
             legs[name] = mfma_entry(ccfg, ms, entry, traffic[name])
             torch.cuda.empty_cache()

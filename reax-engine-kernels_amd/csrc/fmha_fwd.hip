@@ -763,7 +763,9 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
     for (int i = 0; i < 8; ++i) {
       const int row = r0 + 32 * w + 4 * i + lrow0;
       const int u = pu ^ swz(4 * i + lrow0);
-      if (row < Mb) *reinterpret_cast<u32x4_t*>(obase + (long long)tq * p.osT + (long long)gq * p.osG + 8 * u) = x[i];
+      if (row < Mb)
+        __builtin_nontemporal_store(x[i], reinterpret_cast<u32x4_t*>(obase + (long long)tq * p.osT +
+                                                                      (long long)gq * p.osG + 8 * u));
       tq += d4;
       gq += m4;
       if (gq >= p.G) { gq -= p.G; ++tq; }
@@ -842,11 +844,6 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
 // A tile is 16 KB at either head dim: 64 keys at head_dim 128, 32 keys at head_dim 256.
 // BLK0: the drop-in entry points' block rule (all rows of (b, h) form one block of at most 32 rows: when the
 // largest raw qpos among them is 0, every live row sees key 0 only, reax_fmha_v8.cu:155-162, 224-235).
-// ROWS: a prefill too small to fill the GPU with 256-row items (reax_fmha_qx at S 512: 16 items for 256 CUs).
-// The task is then a 32-row block (b, block, KV head) of any p.M, blocks with the most keys first; the workgroup's
-// 4 wavefronts take tiles w, w + 4, ... of the block's key range [0, its largest key limit], and the merge through
-// LDS writes the final O (bf16; 8-byte pieces when o_vec8, i.e. rows 8-byte aligned) and LSE instead of split
-// partials.
 constexpr int DEC_NW = 4;
 
 template <int HD>
@@ -859,9 +856,8 @@ struct DecTile {
   static_assert(TILE == 16384, "two 16 KB tiles per wavefront, four wavefronts: 128 KB of LDS");
 };
 
-template <int HD, bool BLK0, bool ROWS>
-__global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, int wpsplit, int o_vec8) {
-  static_assert(!(BLK0 && ROWS), "the block rule belongs to the drop-in decode");
+template <int HD, bool BLK0>
+__global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, int wpsplit) {
   using T = DecTile<HD>;
   // the K and V tiles of the four wavefronts; after the key loop the same bytes hold the partials being merged
   // (DEC_NW x 32 rows x HD fp32: 64 KB at head_dim 128, all 128 KB at 256)
@@ -874,24 +870,16 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   __shared__ float mm[DEC_NW * 32], lm[DEC_NW * 32];
   const int tid = threadIdx.x, lane = tid & 63, hf = lane >> 5, lr = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wavefront-uniform: keeps the loop control scalar
-  const int P = ROWS ? DEC_NW : wpsplit, part = w % P;
-  const int nrb = ROWS ? (p.M + 31) / 32 : 1;  // 32-row blocks per (b, KV head)
-  const long long ntask = (long long)p.B * (ROWS ? nrb : p.num_splits) * p.H;
+  const int P = wpsplit, part = w % P;
+  const long long ntask = (long long)p.B * p.num_splits * p.H;
   const long long task = (long long)blockIdx.x * (DEC_NW / P) + w / P;
   const bool active = task < ntask;
   const long long tk = active ? task : 0;
-  const int hk = ROWS ? (int)((unsigned)tk % (unsigned)p.H) : (int)(tk % p.H);
-  int split = 0, rb = 0, b = 0;
-  if constexpr (ROWS) {
-    const unsigned t32 = (unsigned)tk, bh = (unsigned)p.B * (unsigned)p.H;  // tk < B * nrb * H <= INT_MAX
-    b = (int)((t32 / (unsigned)p.H) % (unsigned)p.B);
-    rb = nrb - 1 - (int)(t32 / bh);
-  } else {
-    split = (int)((tk / p.H) % p.num_splits);
-    b = (int)(tk / ((long long)p.H * p.num_splits));
-  }
+  const int hk = (int)(tk % p.H);
+  const int split = (int)((tk / p.H) % p.num_splits);
+  const int b = (int)(tk / ((long long)p.H * p.num_splits));
 
-  const int r = rb * 32 + lr;  // row (folded: token r/G, head r%G); without ROWS p.M <= 32 and rb = 0
+  const int r = lr;  // row (folded: token r/G, head r%G); p.M <= 32
   const bool rvalid = r < p.M;
   const int tok = rvalid ? r / p.G : 0, g = rvalid ? r - tok * p.G : 0;
   const uint16_t* Kb = p.k + (long long)b * p.ksB + (long long)hk * p.ksH;
@@ -903,36 +891,15 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   for (int kb = 0; kb < T::NKB; ++kb) kbase[kb] = k_lane_base<HD>(kb, lr, hf);
   const uint32_t vbase = v_lane_base<HD>(lane);
   constexpr int DW = Dma<HD, 1, T::BN>::DW;
-  // a decode split streams its keys once: nontemporal loads; the row blocks of one (b, KV head) all read the same
-  // tiles, which stay in L2 for the next block with ordinary loads
-  constexpr int LK = ROWS ? 1 : 2;
+  // a decode split streams its keys once: nontemporal loads
+  constexpr int LK = 2;
   uint8_t* kb_ = L.k[w];
   uint8_t* vb_ = L.v[w];
   const uint16_t* qrow = p.q + (long long)b * p.qsB + (long long)hk * p.qsH + (long long)tok * p.qsT + (long long)g * p.qsG;
   bf16x8_t qf[T::QK];
-  // tiles t_beg, t_beg + t_step, ... below t_end; keys above a row's lim are masked; tile loads stop at kend
-  int t_beg, t_end, t_step, kend, lim;
-  if constexpr (ROWS) {
-    // tiles part, part + P, ...: the first one does not depend on qpos, so Q, then its K and V, then qpos go out
-    // together (one memory latency; a block seeing fewer tiles leaves the tile unused). Loads complete in issue
-    // order: the wait the compiler puts before qpos's use covers Q and the tile too, and its wait for Q before
-    // the first S^T is then already met.
-    kend = p.N;
-#pragma unroll
-    for (int ks = 0; ks < T::QK; ++ks)
-      qf[ks] = as_bf16x8(rvalid ? ld16(qrow + 16 * ks + 8 * hf) : u32x4_t{0u, 0u, 0u, 0u});
-    if (part * T::BN < p.N) {
-      kplan.template tile<LK>(kb_, Kb, p.ksM, kfast, part * T::BN, kend, 0, lane);
-      vplan.template tile<LK>(vb_, Vb, p.vsM, vfast, part * T::BN, kend, 0, lane);
-    }
-    int qr = -1;
-    if (rvalid && active) qr = p.qpos[(long long)b * p.qpBs + tok];
-    lim = max(min(qr, p.N - 1), -1);
-    const int blim = wave_ext_dpp<true>(lim);
-    t_beg = part;
-    t_end = blim < 0 ? 0 : blim / T::BN + 1;  // key tiles any row of the block sees
-    t_step = P;
-  } else {
+  // tiles t_beg .. t_end - 1; keys above a row's lim are masked; tile loads stop at kend
+  int t_beg, t_end, kend, lim;
+  {
     int qr = -1;
     if (rvalid && active) qr = p.qpos[(long long)b * p.qpBs + tok];
     if (BLK0 && p.N > 0 && wave_max(qr) == 0 && rvalid) qr = 0;  // the block rule: every live row sees key 0
@@ -946,7 +913,6 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
     const int wmax = __builtin_amdgcn_readfirstlane(wave_max(lim));
     t_beg = wbeg / T::BN;
     t_end = wmax < wbeg ? t_beg : wmax / T::BN + 1;
-    t_step = 1;
     // the first K tile, then Q, then the first V tile: one memory latency for all three. Loads return in issue
     // order, so the explicit wait for K(t_beg) before the first S^T (at most the V tile's DW loads outstanding)
     // also covers Q; the waits the compiler adds for Q, which does not count the tile loads, are only stricter.
@@ -956,7 +922,7 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
       qf[ks] = as_bf16x8(rvalid ? ld16(qrow + 16 * ks + 8 * hf) : u32x4_t{0u, 0u, 0u, 0u});
     if (t_end > t_beg) vplan.template tile<2>(vb_, Vb, p.vsM, vfast, t_beg * T::BN, kend, 0, lane);
   }
-  const int wmin = ROWS ? wave_ext_dpp<false>(lim) : __builtin_amdgcn_readfirstlane(wave_min(lim));
+  const int wmin = __builtin_amdgcn_readfirstlane(wave_min(lim));
 
   f32x16_t o[T::DB];
 #pragma unroll
@@ -968,9 +934,9 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   f32x16_t s[T::NKB];
   uint32_t pk[T::NKB][8];
 
-  for (int t = t_beg; t < t_end; t += t_step) {
-    const int k0 = t * T::BN, kn = k0 + t_step * T::BN;  // this tile's first key, the next tile's
-    const bool more = t + t_step < t_end;
+  for (int t = t_beg; t < t_end; ++t) {
+    const int k0 = t * T::BN, kn = k0 + T::BN;  // this tile's first key, the next tile's
+    const bool more = t + 1 < t_end;
     __builtin_amdgcn_s_waitcnt(vmcnt_le(DW));  // K(t) landed (V(t) may be in flight)
 #pragma unroll
     for (int kb = 0; kb < T::NKB; ++kb) {
@@ -1044,85 +1010,6 @@ __global__ void __launch_bounds__(256, 1) fmha_decode_kernel(const FwdParams p, 
   __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
 
   const float l = halves_sum(l_run);
-  if constexpr (ROWS) {
-    // ---- merge of a row block, wavefront w finalising dim block w (HD = 128: 4 blocks of 32 dims). Row maxima
-    // and sums meet in LDS first; every lane (one row) then weights its own partial by
-    //   g_w = 2^(m_w - M) / L,   M = max_w m_w,   L = sum_w 2^(m_w - M) l_w,
-    // so the final O is the plain sum of the weighted partials: each wavefront writes the three dim blocks the
-    // others finalise (48 KB in all, against 64 KB written and read back with the weights applied per element),
-    // reads its own block's three partials and adds its registers. LSE = ln 2 (M + log2 L).
-    static_assert(T::DB == DEC_NW, "one 32-dim block per wavefront");
-    if (hf == 0) {
-      mm[w * 32 + lr] = l > 0.f ? m_run : -INFINITY;
-      lm[w * 32 + lr] = l;
-    }
-    __syncthreads();  // the tile buffers are free, the maxima and sums visible
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < DEC_NW; ++ww) M = fmaxf(M, mm[ww * 32 + lr]);
-    float Lsum = 0.f, gself = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < DEC_NW; ++ww) {
-      const float mw = mm[ww * 32 + lr];
-      const float f = mw == -INFINITY ? 0.f : fast_exp2(mw - M);  // every row maximum -inf: all f are 0
-      Lsum += f * lm[ww * 32 + lr];
-      if (ww == w) gself = f;
-    }
-    const float wt = Lsum > 0.f ? gself / Lsum : 0.f;  // this wavefront's weight g_w
-    // [dim block][source wavefront][32 rows][32 dims] fp32 (64 KB); the 4-dim groups of row x XOR-swizzled by
-    // (x >> 1) & 7 (rows are 128 bytes: rows x and x + 1 cover the two bank halves, the XOR spreads 8 row pairs
-    // over the groups, so a wavefront's 16-byte stores and loads of 16 rows hit 16 distinct bank groups)
-    float* om = reinterpret_cast<float*>(&L);
-    auto oix = [](int db, int src, int x, int grp) {
-      return ((db * DEC_NW + src) * 32 + x) * 32 + ((grp ^ ((x >> 1) & 7)) << 2);
-    };
-#pragma unroll
-    for (int db = 0; db < T::DB; ++db) {
-      if (db == w) continue;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4)
-        *reinterpret_cast<f32x4_t*>(om + oix(db, w, lr, 2 * q4 + hf)) =
-            f32x4_t{o[db][4 * q4 + 0] * wt, o[db][4 * q4 + 1] * wt, o[db][4 * q4 + 2] * wt, o[db][4 * q4 + 3] * wt};
-    }
-    __syncthreads();
-    f32x16_t fin;
-#pragma unroll
-    for (int db = 0; db < T::DB; ++db)
-      if (db == w)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) fin[e] = o[db][e] * wt;
-#pragma unroll
-    for (int src = 0; src < DEC_NW; ++src) {
-      if (src == w) continue;
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const f32x4_t a = *reinterpret_cast<const f32x4_t*>(om + oix(w, src, lr, 2 * q4 + hf));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) fin[4 * q4 + e] += a[e];
-      }
-    }
-    if (!rvalid) return;
-    if (p.lse && w == 0 && hf == 0)
-      p.lse[(long long)b * p.lsB + (long long)hk * p.lsH + (long long)tok * p.lsT + (long long)g * p.lsG] =
-          Lsum > 0.f ? (M + log2f(Lsum)) * 0.69314718055994530942f : -INFINITY;
-    if (!p.o) return;
-    // row r, dims 32 w + 8 q4 + 4 hf .. + 3: one 8-byte piece per q4 (two 4-byte pieces when rows are only
-    // 4-byte aligned)
-    uint16_t* orow = p.o + (long long)b * p.osB + (long long)hk * p.osH + (long long)tok * p.osT +
-                     (long long)g * p.osG + 32 * w + 4 * hf;
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const uint32_t w0 = pack_bf16x2(fin[4 * q4 + 0], fin[4 * q4 + 1]);
-      const uint32_t w1 = pack_bf16x2(fin[4 * q4 + 2], fin[4 * q4 + 3]);
-      if (o_vec8) {
-        *reinterpret_cast<u32x2_t*>(orow + 8 * q4) = u32x2_t{w0, w1};
-      } else {
-        reinterpret_cast<uint32_t*>(orow + 8 * q4)[0] = w0;
-        reinterpret_cast<uint32_t*>(orow + 8 * q4)[1] = w1;
-      }
-    }
-    return;
-  }
   // ---- merge the P partials of each split through LDS (the tile buffers are free once every wavefront is here)
   __syncthreads();
   // [DEC_NW][32 rows][HD], 16-byte groups of row x XOR-swizzled by x & 15: a wavefront's stores of 4 dims of its
@@ -1358,13 +1245,249 @@ static int launch_fwd_pp(FwdParams p, hipStream_t stream) {
   return (int)hipGetLastError();
 }
 
-// The row-block form of the decode kernel (head_dim 128, qpos mode): one 4-wavefront workgroup per 32-row block.
+// ------------------------------------------------------------------------------------------------------------
+// Row-block prefill for small head_dim-128 qpos calls (reax_fmha_qx at S 512: the ping-pong kernel's 256-row items
+// would fill 16 of 256 CUs). The task is a 32-row block (b, block, KV head), blocks with the most keys first, one
+// 8-wavefront workgroup per block: wavefront w takes the 32-key tiles w, w + 8, ... of the block's key range
+// [0, its largest key limit], each through its own 8 KB K and V buffers (the next tile's K loads as soon as the
+// current S^T has read K, its V after P.V). Two wavefronts per SIMD: while one waits for its tile copies (the CU's
+// vector memory path carries the heaviest block's whole K/V range, 256 KB at S 512), the other computes. Q crosses
+// once through LDS (one 1 KB copy per wavefront). The eight partials merge through the tile buffers: each
+// wavefront, as its key loop ends, writes its partial into its own buffers; after one barrier wavefront w
+// finalises the 8 values per lane of dim block w / 2, half w % 2, weighting and adding the eight partials' slices
+// (112 KB through LDS).
+constexpr int RB_NW = 8;
+constexpr int RB_BN = 32;
+
+__global__ void __launch_bounds__(64 * RB_NW, 1) fmha_rows_kernel(const FwdParams p, int o_vec8) {
+  constexpr int HD = 128, BN = RB_BN, TILE = BN * HD * 2, QK = HD / 16, DB = HD / 32;
+  using DmaT = Dma<HD, 1, BN>;
+  constexpr int DW = DmaT::DW;  // 8 loads per tile
+  struct Lds {
+    uint8_t k[RB_NW][TILE];
+    uint8_t v[RB_NW][TILE];
+  };
+  // after its key loop a wavefront's K and V buffers hold its partial for the merge: 16 slots of 64 x 16 bytes
+  static_assert(TILE == 8 * 1024, "8 merge slots per tile buffer");
+  __shared__ __align__(1024) Lds L;
+  __shared__ __align__(1024) uint8_t qs[32 * HD * 2];  // the block's Q rows, swizzled as a 32-row K tile
+  __shared__ float mm[RB_NW * 32], lm[RB_NW * 32];
+  const int tid = threadIdx.x, lane = tid & 63, hf = lane >> 5, lr = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nrb = (p.M + 31) / 32;
+  const unsigned t32 = blockIdx.x, bhn = (unsigned)p.B * (unsigned)p.H;  // blockIdx.x < B * nrb * H
+  const int hk = (int)(t32 % (unsigned)p.H);
+  const int b = (int)((t32 / (unsigned)p.H) % (unsigned)p.B);
+  const int rb = nrb - 1 - (int)(t32 / bhn);
+  const int r = rb * 32 + lr;
+  const bool rvalid = r < p.M;
+  const int tok = rvalid ? r / p.G : 0, g = rvalid ? r - tok * p.G : 0;
+  const uint16_t* Kb = p.k + (long long)b * p.ksB + (long long)hk * p.ksH;
+  const uint16_t* Vb = p.v + (long long)b * p.vsB + (long long)hk * p.vsH;
+  const DmaT kplan(p.ksM, 0, lane), vplan(p.vsM, 0, lane);
+  const bool kfast = p.ksM * 2 * BN < (1ll << 31), vfast = p.vsM * 2 * BN < (1ll << 31);
+  uint8_t* kb_ = L.k[w];
+  uint8_t* vb_ = L.v[w];
+  {
+    // Q copy w: rows 4w .. 4w + 3 of the block (lane l: row 4w + l / 16, logical unit (l % 16) ^ swz(row)); rows
+    // past the end read the last row (never stored)
+    const int lrow = 4 * w + (lane >> 4), pu = lane & 15;
+    const int rr = min(rb * 32 + lrow, p.M - 1);
+    const int tq = rr / p.G, gq = rr - tq * p.G;
+    const uint16_t* src = p.q + (long long)b * p.qsB + (long long)hk * p.qsH + (long long)tq * p.qsT +
+                          (long long)gq * p.qsG + 8 * (pu ^ swz(lrow));
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(&qs[w * 1024]));
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(m0) : "memory");
+  }
+  // the first tile does not depend on qpos: its K and V go out with Q, then qpos (loads complete in issue order,
+  // and the wait the compiler puts before qpos's use, which does not count the copies, drains them all)
+  if (w * BN < p.N) {
+    kplan.template tile<1>(kb_, Kb, p.ksM, kfast, w * BN, p.N, 0, lane);
+    vplan.template tile<1>(vb_, Vb, p.vsM, vfast, w * BN, p.N, 0, lane);
+  }
+  int qr = -1;
+  if (rvalid) qr = p.qpos[(long long)b * p.qpBs + tok];
+  const int lim = max(min(qr, p.N - 1), -1);
+  const int blim = wave_ext_dpp<true>(lim);  // every wavefront holds the same 32 rows
+  const int wmin = wave_ext_dpp<false>(lim);
+  const int t_end = blim < 0 ? 0 : blim / BN + 1;  // key tiles any row of the block sees
+  __builtin_amdgcn_s_waitcnt(0x0F70);              // vmcnt(0): this wavefront's Q copy (and its first tile)
+  __syncthreads();                                 // ... and every other wavefront's Q copy
+  bf16x8_t qf[QK];
+  {
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const uint32_t qa = (uint32_t)reinterpret_cast<uintptr_t>(&qs[0]) + k_lane_base<HD>(0, ln & 31, ln >> 5);
+#pragma unroll
+    for (int ks = 0; ks < QK; ++ks)
+      qf[ks] = as_bf16x8(*reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(qa ^ (32u * ks)));
+  }
+  const uint32_t kbase = k_lane_base<HD>(0, lr, hf);
+  const uint32_t vbase = v_lane_base<HD>(lane);
+
+  f32x16_t o[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[db][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+  const float cc = p.scale_log2;
+  f32x16_t s;
+  uint32_t pk[8];
+  for (int t = w; t < t_end; t += RB_NW) {
+    const int k0 = t * BN, kn = k0 + RB_NW * BN;
+    const bool more = t + RB_NW < t_end;
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(DW));  // K(t) landed (V(t) may be in flight)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s[e] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < QK; ++ks) {
+      const u32x4_t kf = *reinterpret_cast<const u32x4_t*>(kb_ + (kbase ^ (32u * ks)));
+      s = mfma32(as_bf16x8(kf), qf[ks], s);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the K tile has been read
+    if (more) kplan.template tile<1>(kb_, Kb, p.ksM, kfast, kn, p.N, 0, lane);
+    if (k0 + BN - 1 > wmin) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int key = k0 + 8 * (v >> 2) + 4 * hf + (v & 3);
+        if (key > lim) s[v] = -INFINITY;
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[v]);
+    mx = halves_max(mx) * cc;
+    if (__any(mx > m_run + RESCALE_SLACK)) {
+      const float m_new = fmaxf(m_run, mx);
+      if (__any(m_run != -INFINITY)) {  // before the first admitted key O and the sums are still 0
+        const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[db][e] *= alpha;
+      }
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float ps[2] = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float p0 = fast_exp2(__builtin_fmaf(s[2 * i], cc, -m_use));
+      const float p1 = fast_exp2(__builtin_fmaf(s[2 * i + 1], cc, -m_use));
+      ps[i & 1] += p0 + p1;
+      pk[i] = pack_bf16x2(p0, p1);
+    }
+    l_run += ps[0] + ps[1];
+    if (more)
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(DW));  // V(t) landed, K(t+8) may be in flight
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss) {
+      const bf16x8_t pb = as_bf16x8(u32x4_t{pk[4 * ss], pk[4 * ss + 1], pk[4 * ss + 2], pk[4 * ss + 3]});
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[db] = mfma32(v_operand<HD>(vb_, db, ss, vbase), pb, o[db]);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the V tile has been read
+    if (more) vplan.template tile<1>(vb_, Vb, p.vsM, vfast, kn, p.N, 0, lane);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+
+  // ---- merge: O = sum_w f_w O_w / L, f_w = 2^(m_w - M), M = max_w m_w, L = sum_w f_w l_w. As soon as its key
+  // loop ends, wavefront w writes its unweighted partial into its own tile buffers (free now, and read by no
+  // other wavefront): slice d (dim block d / 2, values 8 (d % 2) .. + 7 of each lane's 16, finalised by
+  // wavefront d) as two 16-byte pieces per lane in 1 KB slot 2 d + q (slots 0-7 in its K buffer, 8-15 in its V
+  // buffer; consecutive lanes 16 bytes apart), its own slot unused. One barrier, then wavefront w weights and
+  // adds the seven slices of its own slot.
+  const float l = halves_sum(l_run);
+  if (hf == 0) {
+    mm[w * 32 + lr] = l > 0.f ? m_run : -INFINITY;
+    lm[w * 32 + lr] = l;
+  }
+  auto slot = [&](int src, int sl) __attribute__((always_inline)) {
+    return reinterpret_cast<u32x4_t*>(sl < 8 ? &L.k[src][sl * 1024] : &L.v[src][(sl - 8) * 1024]) + lane;
+  };
+#pragma unroll
+  for (int d = 0; d < RB_NW; ++d) {
+    if (d == w) continue;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const f32x16_t& od = o[d >> 1];
+      const int v0 = 8 * (d & 1) + 4 * q;
+      *slot(w, 2 * d + q) = u32x4_t{__float_as_uint(od[v0]), __float_as_uint(od[v0 + 1]),
+                                    __float_as_uint(od[v0 + 2]), __float_as_uint(od[v0 + 3])};
+    }
+  }
+  __syncthreads();  // every partial, row maximum and sum visible
+  // all slice reads first (the own slot's too, never written: its values are not used), so that their LDS
+  // latencies overlap each other and the row maxima's
+  u32x4_t sl[RB_NW][2];
+#pragma unroll
+  for (int src = 0; src < RB_NW; ++src)
+#pragma unroll
+    for (int q = 0; q < 2; ++q) sl[src][q] = *slot(src, 2 * w + q);
+  float ms[RB_NW], ls[RB_NW];
+#pragma unroll
+  for (int src = 0; src < RB_NW; ++src) {
+    ms[src] = mm[src * 32 + lr];
+    ls[src] = lm[src * 32 + lr];
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int src = 0; src < RB_NW; ++src) M = fmaxf(M, ms[src]);
+  float fin[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float Lsum = 0.f, fself = 0.f;
+#pragma unroll
+  for (int src = 0; src < RB_NW; ++src) {
+    const float f = ms[src] == -INFINITY ? 0.f : fast_exp2(ms[src] - M);  // every row maximum -inf: all f are 0
+    Lsum += f * ls[src];
+    if (src == w) {
+      fself = f;
+      continue;
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) fin[4 * q + e] = __builtin_fmaf(f, __uint_as_float(sl[src][q][e]), fin[4 * q + e]);
+  }
+#pragma unroll
+  for (int d = 0; d < RB_NW; ++d)
+    if (d == w)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) fin[e] = __builtin_fmaf(fself, o[d >> 1][8 * (d & 1) + e], fin[e]);
+  const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) fin[e] *= inv;
+  if (!rvalid) return;
+  if (p.lse && w == 0 && hf == 0)
+    p.lse[(long long)b * p.lsB + (long long)hk * p.lsH + (long long)tok * p.lsT + (long long)g * p.lsG] =
+        Lsum > 0.f ? (M + log2f(Lsum)) * 0.69314718055994530942f : -INFINITY;
+  if (!p.o) return;
+  // values 8 (w % 2) + 4 q + e of dim block w / 2 are dims 32 (w / 2) + 8 (2 (w % 2) + q) + 4 hf + e: one 8-byte
+  // piece per q (two 4-byte pieces when rows are only 4-byte aligned)
+  uint16_t* orow = p.o + (long long)b * p.osB + (long long)hk * p.osH + (long long)tok * p.osT +
+                   (long long)g * p.osG + 32 * (w >> 1) + 16 * (w & 1) + 4 * hf;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const uint32_t w0 = pack_bf16x2(fin[4 * q + 0], fin[4 * q + 1]);
+    const uint32_t w1 = pack_bf16x2(fin[4 * q + 2], fin[4 * q + 3]);
+    if (o_vec8) {
+      __builtin_nontemporal_store(u32x2_t{w0, w1}, reinterpret_cast<u32x2_t*>(orow + 8 * q));
+    } else {
+      __builtin_nontemporal_store(w0, reinterpret_cast<uint32_t*>(orow + 8 * q));
+      __builtin_nontemporal_store(w1, reinterpret_cast<uint32_t*>(orow + 8 * q) + 1);
+    }
+  }
+}
+
+// The row-block kernel (head_dim 128, qpos mode): one 8-wavefront workgroup per 32-row block.
 static int launch_fwd_rows(const FwdParams& p, hipStream_t stream) {
   const long long nwg = (long long)p.B * p.H * ((p.M + 31) / 32);
   if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
   const int o_vec8 = p.o && aligned_elems(p.o, 4, {p.osB, p.osH, p.osT, p.osG}) ? 1 : 0;  // 8-byte output pieces
-  hipLaunchKernelGGL((fmha_decode_kernel<128, false, true>), dim3((unsigned)nwg), dim3(64 * DEC_NW), 0, stream, p,
-                     DEC_NW, o_vec8);
+  hipLaunchKernelGGL(fmha_rows_kernel, dim3((unsigned)nwg), dim3(64 * RB_NW), 0, stream, p, o_vec8);
   return (int)hipGetLastError();
 }
 
@@ -1458,11 +1581,11 @@ int launch_decode_split(FwdParams p, int head_dim, int P, bool post, hipStream_t
   if (nwg <= 0 || nwg > INT_MAX) return (int)hipErrorInvalidConfiguration;
   if (head_dim == 128) {
     if (post || p.qpos0_block) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL((fmha_decode_kernel<128, false, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P, 0);
+    hipLaunchKernelGGL((fmha_decode_kernel<128, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
   } else if (p.qpos0_block) {
-    hipLaunchKernelGGL((fmha_decode_kernel<256, true, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P, 0);
+    hipLaunchKernelGGL((fmha_decode_kernel<256, true>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
   } else {
-    hipLaunchKernelGGL((fmha_decode_kernel<256, false, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P, 0);
+    hipLaunchKernelGGL((fmha_decode_kernel<256, false>), dim3((unsigned)nwg), dim3(256), 0, stream, p, P);
   }
   if (const int rc = (int)hipGetLastError()) return rc;
   return launch_combine(p, head_dim, post, stream);

@@ -205,9 +205,10 @@ def test_qx_output_strides(pad, B, Hq, Hkv, route):
 
 
 # The row-block kernel (head_dim-128 prefills too small to fill the GPU with 256-row items): 32-row blocks, the
-# block's keys cut into 4 runs of 64-key tiles, one per wavefront, merged in LDS. Partial last blocks, fewer rows
-# than a block, G = 1 and 16, key ranges of one tile to 65 (a partial last tile), runs left empty (a block seeing
-# fewer tiles than there are wavefronts), random qpos with negatives and qpos >= N, and no LSE output.
+# block's 32-key tiles dealt to 8 wavefronts (tiles w, w + 8, ...), merged in LDS. Partial last blocks, fewer rows
+# than a block, G = 1 and 16, key ranges of one tile to 129 tiles (a partial last tile; up to 17 tiles per
+# wavefront), wavefronts left without a tile (a block seeing fewer tiles than there are wavefronts), random qpos
+# with negatives and qpos >= N, and no LSE output.
 ROWS = [
     FC.Case("rows_ragged_b3_s77", B=3, S=77, N=77, Hq=8, Hkv=2, D=128, mode="causal", seed=51),
     FC.Case("rows_m24_n4100", B=2, S=3, N=4100, Hq=16, Hkv=2, D=128, mode="full", seed=52),
