@@ -1255,7 +1255,7 @@ static int launch_fwd_pp(FwdParams p, hipStream_t stream) {
 // once through LDS (one 1 KB copy per wavefront). The eight partials merge through the tile buffers: each
 // wavefront, as its key loop ends, writes its partial into its own buffers; after one barrier wavefront w
 // finalises the 8 values per lane of dim block w / 2, half w % 2, weighting and adding the eight partials' slices
-// (112 KB through LDS).
+// (128 KB through LDS).
 constexpr int RB_NW = 8;
 constexpr int RB_BN = 32;
 
@@ -1399,8 +1399,8 @@ __global__ void __launch_bounds__(64 * RB_NW, 1) fmha_rows_kernel(const FwdParam
   // loop ends, wavefront w writes its unweighted partial into its own tile buffers (free now, and read by no
   // other wavefront): slice d (dim block d / 2, values 8 (d % 2) .. + 7 of each lane's 16, finalised by
   // wavefront d) as two 16-byte pieces per lane in 1 KB slot 2 d + q (slots 0-7 in its K buffer, 8-15 in its V
-  // buffer; consecutive lanes 16 bytes apart), its own slot unused. One barrier, then wavefront w weights and
-  // adds the seven slices of its own slot.
+  // buffer; consecutive lanes 16 bytes apart), its own slice included. One barrier, then wavefront w weights and
+  // adds the eight slices of slot 2 w + q, with no per-wavefront branch or register selection.
   const float l = halves_sum(l_run);
   if (hf == 0) {
     mm[w * 32 + lr] = l > 0.f ? m_run : -INFINITY;
@@ -1411,7 +1411,6 @@ __global__ void __launch_bounds__(64 * RB_NW, 1) fmha_rows_kernel(const FwdParam
   };
 #pragma unroll
   for (int d = 0; d < RB_NW; ++d) {
-    if (d == w) continue;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       const f32x16_t& od = o[d >> 1];
@@ -1421,8 +1420,7 @@ __global__ void __launch_bounds__(64 * RB_NW, 1) fmha_rows_kernel(const FwdParam
     }
   }
   __syncthreads();  // every partial, row maximum and sum visible
-  // all slice reads first (the own slot's too, never written: its values are not used), so that their LDS
-  // latencies overlap each other and the row maxima's
+  // all slice reads first, so that their LDS latencies overlap each other and the row maxima's
   u32x4_t sl[RB_NW][2];
 #pragma unroll
   for (int src = 0; src < RB_NW; ++src)
@@ -1438,25 +1436,16 @@ __global__ void __launch_bounds__(64 * RB_NW, 1) fmha_rows_kernel(const FwdParam
 #pragma unroll
   for (int src = 0; src < RB_NW; ++src) M = fmaxf(M, ms[src]);
   float fin[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float Lsum = 0.f, fself = 0.f;
+  float Lsum = 0.f;
 #pragma unroll
   for (int src = 0; src < RB_NW; ++src) {
     const float f = ms[src] == -INFINITY ? 0.f : fast_exp2(ms[src] - M);  // every row maximum -inf: all f are 0
     Lsum += f * ls[src];
-    if (src == w) {
-      fself = f;
-      continue;
-    }
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
       for (int e = 0; e < 4; ++e) fin[4 * q + e] = __builtin_fmaf(f, __uint_as_float(sl[src][q][e]), fin[4 * q + e]);
   }
-#pragma unroll
-  for (int d = 0; d < RB_NW; ++d)
-    if (d == w)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) fin[e] = __builtin_fmaf(fself, o[d >> 1][8 * (d & 1) + e], fin[e]);
   const float inv = Lsum > 0.f ? 1.0f / Lsum : 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) fin[e] *= inv;
