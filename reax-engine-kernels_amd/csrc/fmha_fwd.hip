@@ -1462,11 +1462,13 @@ __global__ void __launch_bounds__(64 * RB_NW, 1) fmha_rows_kernel(const FwdParam
   for (int q = 0; q < 2; ++q) {
     const uint32_t w0 = pack_bf16x2(fin[4 * q + 0], fin[4 * q + 1]);
     const uint32_t w1 = pack_bf16x2(fin[4 * q + 2], fin[4 * q + 3]);
+    // ordinary stores: each wavefront writes 32 bytes of a row, and the L2 merges the eight wavefronts' pieces into
+    // whole lines (as nontemporal stores the pieces reach HBM separately: 1.55 MB written instead of 1.04)
     if (o_vec8) {
-      __builtin_nontemporal_store(u32x2_t{w0, w1}, reinterpret_cast<u32x2_t*>(orow + 8 * q));
+      *reinterpret_cast<u32x2_t*>(orow + 8 * q) = u32x2_t{w0, w1};
     } else {
-      __builtin_nontemporal_store(w0, reinterpret_cast<uint32_t*>(orow + 8 * q));
-      __builtin_nontemporal_store(w1, reinterpret_cast<uint32_t*>(orow + 8 * q) + 1);
+      reinterpret_cast<uint32_t*>(orow + 8 * q)[0] = w0;
+      reinterpret_cast<uint32_t*>(orow + 8 * q)[1] = w1;
     }
   }
 }
