@@ -656,7 +656,11 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
     // tile per step, no per-step flags. t_fast is per wavefront; every step, fast or not, has the same two
     // barriers, so the wavefronts stay in step.
     int t_fast = 0;
-    if (MODE != MODE_VARLEN && kfast && vfast) {
+    // the fast steps form their load sources with 32-bit byte offsets from the tile bases (one scalar multiply
+    // per tile instead of a 64-bit product): every wavefront runs this scalar arithmetic after the same barrier,
+    // through the CU's one scalar unit
+    const bool off32 = (long long)Nb * p.ksM * 2 < (1ll << 32) && (long long)Nb * p.vsM * 2 < (1ll << 32);
+    if (MODE != MODE_VARLEN && kfast && vfast && off32) {
       const int lm = min(wmin, wmax);  // wmax < 0: no row of the wavefront sees a key
       t_fast = min(min(t_end - 2, Nb / T::BN - 2), lm >= T::BN - 1 ? (lm + 1) / T::BN - 1 : 0);
     }
@@ -693,11 +697,12 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
     };
     static_assert(NS == 2, "the fast steps alternate two K/V buffers");
     // step t loads K(t+1) and V(t)
+    const uint32_t ktile = (uint32_t)(T::BN * 2) * (uint32_t)p.ksM, vtile = (uint32_t)(T::BN * 2) * (uint32_t)p.vsM;
     auto ksrc_of = [&](int t) __attribute__((always_inline)) {
-      return reinterpret_cast<const uint8_t*>(Kb + (long long)(t + 1) * T::BN * p.ksM);
+      return reinterpret_cast<const uint8_t*>(Kb) + (uint32_t)(t + 1) * ktile;
     };
     auto vsrc_of = [&](int t) __attribute__((always_inline)) {
-      return reinterpret_cast<const uint8_t*>(Vb + (long long)t * T::BN * p.vsM);
+      return reinterpret_cast<const uint8_t*>(Vb) + (uint32_t)t * vtile;
     };
     if constexpr (MODE == MODE_VARLEN) {
       for (int t = 0; t <= t_end; t += NS) {
