@@ -377,8 +377,9 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   const int BH = p.B * p.H;
   const long long n_items = (long long)BH * p.n_tiles;
   const bool xcd_aware = MODE != MODE_VARLEN && (BH & 7) == 0 && (gridDim.x & 7) == 0;
-  // item (bh, tile): row tile `tile` of (batch or sequence bh / H, KV head bh % H)
-  auto item = [&](int bh, int tile) __attribute__((always_inline)) {
+  // item (bh, tile): row tile `tile` of (batch or sequence bh / H, KV head bh % H). with_rounds (varlen only): the
+  // schedule's rounds run in wavefront 0 while this item's first loads are in flight, before its first barrier
+  auto item = [&](int bh, int tile, bool with_rounds) __attribute__((always_inline)) {
   const int b = bh / p.H, hk = bh - b * p.H;
   long long tok0 = 0;
   int Mb = p.M, Nb = p.N;
@@ -389,7 +390,15 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
     Mb = Nb * p.G;
   }
   const int r0 = tile * PP_BM;
-  if (r0 >= Mb) return;  // uniform over the workgroup
+  if (r0 >= Mb) {  // uniform over the workgroup
+    if constexpr (MODE == MODE_VARLEN) {
+      if (with_rounds) {
+        vs_rounds(vs, gridDim.x, blockIdx.x);
+        __syncthreads();
+      }
+    }
+    return;
+  }
 
   const int r = r0 + 32 * w + lr;
   const bool rvalid = r < Mb;
@@ -437,6 +446,9 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
   // they must not force the mask pass onto every key tile of a partial row tile.
   const int wmax = wave_max(lim), wmin = wave_min(rvalid ? lim : INT_MAX);
   if (lane == 0) s_lim[w] = wmax;
+  if constexpr (MODE == MODE_VARLEN) {
+    if (with_rounds) vs_rounds(vs, gridDim.x, blockIdx.x);  // the barrier below orders S.mine[] before its reads
+  }
   // the Q and K(0) copies are inline assembly, which the compiler does not count: wait for them explicitly
   // (the barrier's own fence only drains the loads it knows of)
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -800,11 +812,17 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
     // packed sequences: the longest-first schedule of fmha_sched.h, computed alike by every workgroup
     vs_build<PP_BM>(vs, p.cu_seqlens, p.B, p.H, p.G, P, (int)blockIdx.x);
     if (vs.ok) {
+      // round 0's item is known from the tables; the later rounds are worked out during its prologue
+      const int first = vs_first(vs, P, (int)blockIdx.x);
+      if (first < 0) {
+        vs_rounds(vs, P, (int)blockIdx.x);
+        __syncthreads();
+      }
       for (int r = 0; r < vs.rounds; ++r) {
-        const int v = vs.mine[r];  // sequence * H + KV head, times 1024, plus row tile
+        const int v = r == 0 ? first : vs.mine[r];  // sequence * H + KV head, times 1024, plus row tile
         if (v < 0) continue;
         exec_barrier();  // as below
-        item(v >> 10, v & 1023);
+        item(v >> 10, v & 1023, r == 0);
       }
       return;
     }
@@ -832,7 +850,7 @@ __global__ void __launch_bounds__(512, 1) fmha_fwd_pp_kernel(const FwdParams p, 
     // full barrier). Not __syncthreads(): its fence would wait for the previous item's output stores, whose
     // latency instead overlaps the next item's first loads.
     exec_barrier();
-    item(bh, p.n_tiles - 1 - rank);
+    item(bh, p.n_tiles - 1 - rank, false);
   }
 }
 

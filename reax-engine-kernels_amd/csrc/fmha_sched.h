@@ -20,7 +20,8 @@
 //      the least work (in increasing order of that work, ties by index).
 // Steps 1-3 build tables (the class's pairs, their prefix sums, the level starts, and each item's identity and
 // cost) with every thread of the workgroup, and the rounds run in one wavefront, each a rank scan of the loads
-// (kept as distinct keys, load * 256 + index) and one table read. On config 3 (stamped copy of the kernel) the
+// (kept as distinct keys, load * 256 + index) and one table read. Round 0's item follows from the tables alone, so
+// the kernel issues that item's first loads before the rounds and runs them while the loads are in flight. On config 3 (stamped copy of the kernel) the
 // schedule takes ~5.8 us before the first item, against ~7 us when each round decoded its items and compared
 // (load, index) pairs, and the busiest workgroup's items ~54 us, against ~56 us when every round handed out PW
 // items (half rounds get as close as one-item-at-a-time LPT, in a few rounds): 0.0722 -> 0.0677 ms.
@@ -75,8 +76,9 @@ __device__ __forceinline__ int vs_cost(int tpl, int L, int level) {
   return 2 * (last / 64 + 1) + 5;
 }
 
-// Builds this workgroup's schedule (every thread of the workgroup calls it; it ends with a barrier). Sets S.ok = 0
-// when the shape exceeds the tables. wg is the workgroup index, P the grid size.
+// Builds the schedule's tables (every thread of the workgroup calls it; it ends with a barrier). Sets S.ok = 0 when
+// the shape exceeds the tables. wg is the workgroup index, P the grid size. With S.ok set, this workgroup's round-0
+// item is vs_first(S, P, wg) right away; vs_rounds then fills S.mine[].
 template <int BM>
 __device__ void vs_build(VarlenSched& S, const int* cu, int nseq, int H, int G, int P, int wg) {
   const int tid = threadIdx.x, nt = blockDim.x;
@@ -181,9 +183,23 @@ __device__ void vs_build(VarlenSched& S, const int* cu, int nseq, int H, int G, 
     S.kcost[k] = vs_cost(tpl, S.pL[q], lo);
   }
   __syncthreads();
+}
+
+// This workgroup's item from round 0 (as kitem, -1 for none): every load starts at zero work, so the rank of class
+// workgroup m's key (0 * 256 + m) is m, and round 0 gives it item m.
+__device__ __forceinline__ int vs_first(const VarlenSched& S, int P, int wg) {
+  const int me = wg / ((P % 8 == 0) ? 8 : 1);
+  return me < S.nreal ? S.kitem[me] : -1;
+}
+
+// The rounds, in wavefront 0 alone (every thread may call it; threads of the other wavefronts return at once). Its
+// LDS accesses complete in issue order, so no barrier is needed between a round's reads and writes; the caller
+// puts a workgroup barrier between this call and any read of S.mine[]. Needs the tables of vs_build with S.ok set.
+__device__ void vs_rounds(VarlenSched& S, int P, int wg) {
+  const int tid = threadIdx.x;
+  const int nx = (P % 8 == 0) ? 8 : 1, pw = P / nx, me = wg / nx, nreal = S.nreal;
   if (tid < 64) {
-    // the rounds, in wavefront 0 alone (its LDS accesses complete in issue order, so no barrier is needed between
-    // a round's reads and writes): lane l stands for class workgroups l, l + 64, l + 128, l + 192
+    // lane l stands for class workgroups l, l + 64, l + 128, l + 192
     const int lane = tid, hb = max(1, pw / 2), rounds = S.rounds;
     for (int r = 0; r < rounds; ++r) {
       const int base = r == 0 ? 0 : pw + (r - 1) * hb, batch = r == 0 ? pw : hb;
@@ -225,7 +241,6 @@ __device__ void vs_build(VarlenSched& S, const int* cu, int nseq, int H, int G, 
       asm volatile("" ::: "memory");  // and its writes before the next round's reads
     }
   }
-  __syncthreads();
 }
 
 }  // namespace reax
