@@ -1509,7 +1509,7 @@ int launch_fwd(const FwdParams& p0, int head_dim, int mode, bool post, hipStream
   FwdParams p = p0;
   if (const int rc = prepare(p, post)) return rc;
   // head_dim 128 qpos prefills whose 256-row items would occupy at most a quarter of the CUs (config 1: 16 items):
-  // 32-row blocks with their keys split over 4 wavefronts, 8 times the workgroups of the ping-pong kernel
+  // 32-row blocks with their keys split over 8 wavefronts, 8 times the workgroups of the ping-pong kernel
   if (head_dim == 128 && !post && !p.qpos0_block && mode == MODE_QPOS) {
     const long long pp_items = (long long)p.B * p.H * (((long long)p.M + PP_BM - 1) / PP_BM);
     if (pp_items > 0) {
@@ -1518,8 +1518,8 @@ int launch_fwd(const FwdParams& p0, int head_dim, int mode, bool post, hipStream
     }
   }
   // head_dim 128 qpos / varlen without the POST epilogue: the ping-pong kernel once a row tile has enough rows
-  // to fill both groups (short query blocks, e.g. decode, keep the 4-wavefront kernel); the drop-in block rule
-  // (qpos0_block) lives in the 4-wavefront kernel only
+  // to fill both groups (short query blocks, e.g. decode, keep the 4-wavefront kernel); it has no drop-in block
+  // rule (qpos0_block), which the 4-wavefront, pair and decode kernels implement
   if (head_dim == 128 && !post && !p.qpos0_block && p.M > FwdTile<128>::BM) {
     if (mode == MODE_QPOS) return launch_fwd_pp<MODE_QPOS>(p, stream);
     if (mode == MODE_VARLEN) return launch_fwd_pp<MODE_VARLEN>(p, stream);
