@@ -1,6 +1,7 @@
 """CPU: the drop-in boundary. The two libraries load, export exactly the functions their headers declare (the
-reference's names plus the declared extensions), set no soname, and return the documented codes for calls that
-touch no GPU (NULL bias, the argument guards of the GDN / norm / conv entry points, workspace sizing)."""
+reference's names plus the declared extensions), set no soname, bind every argument with the ctypes type of its C
+prototype, and return the documented codes for calls that touch no GPU (NULL bias, the argument guards of the GDN /
+norm / conv entry points, workspace sizing)."""
 import ctypes
 import os
 import re
@@ -207,3 +208,39 @@ def test_gemm_config_names_cover_the_tiles():
         assert all(x.startswith("mfma ") for x in names), (name, names)
         assert names[0].startswith("mfma 256x256x64"), (name, names[0])
         assert len(set(names)) == 5, (name, sorted(set(names)))
+
+
+def prototypes(header):
+    """name -> (return type, argument declarations) of every function the header declares."""
+    text = open(os.path.join(INC, header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    out = {}
+    for m in re.finditer(r"^\s*((?:const\s+)?(?:int|size_t|char|void)\s*\*?)\s*(\w+)\s*\(([^;]*?)\)\s*;", text,
+                         flags=re.M | re.S):
+        args = m.group(3).strip()
+        out[m.group(2)] = (re.sub(r"\s+", " ", m.group(1).strip()),
+                           [] if args in ("", "void") else [re.sub(r"\s+", " ", a.strip()) for a in args.split(",")])
+    return out
+
+
+def c_to_ctypes(decl):
+    """The ctypes type the loader must bind for one C argument declaration (every pointer and the stream: c_void_p)."""
+    if "*" in decl or decl.startswith("hipStream_t"):
+        return ctypes.c_void_p
+    base = re.sub(r"\s\w+$", "", decl)  # the type without the argument's name
+    return {"int": ctypes.c_int, "long long": ctypes.c_longlong, "float": ctypes.c_float,
+            "size_t": ctypes.c_size_t}[base]
+
+
+@pytest.mark.parametrize("header", sorted(h for h in os.listdir(INC) if h.endswith(".h")))
+def test_binding_argtypes_match_prototypes(header):
+    # the ctypes binding (abi.SIGNATURES / abi.RESTYPES) against the C prototypes, argument by argument: a count or
+    # width mismatch would shift every later argument of the call
+    protos = prototypes(header)
+    assert protos, f"no prototypes parsed from {header}"
+    assert set(declared(header)) <= set(protos), "a prototype the parser missed"
+    for name, (ret, args) in protos.items():
+        assert abi.SIGNATURES[name] == [c_to_ctypes(a) for a in args], name
+        want_ret = {"int": None, "size_t": ctypes.c_size_t, "const char*": ctypes.c_char_p}[ret]
+        assert abi.RESTYPES.get(name) == want_ret, name
