@@ -244,3 +244,13 @@ def test_binding_argtypes_match_prototypes(header):
         assert abi.SIGNATURES[name] == [c_to_ctypes(a) for a in args], name
         want_ret = {"int": None, "size_t": ctypes.c_size_t, "const char*": ctypes.c_char_p}[ret]
         assert abi.RESTYPES.get(name) == want_ret, name
+
+
+def test_integration_doc_argtypes_match_binding():
+    # INTEGRATION.md shows the loader's argtypes lines for a maintainer to copy: each must equal the binding's
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    names = {"P": ctypes.c_void_p, "I": ctypes.c_int, "LL": ctypes.c_longlong, "F": ctypes.c_float, "ctypes": ctypes}
+    lines = re.findall(r"^\w+\.(\w+)\.argtypes = (.+)$", text, flags=re.M)
+    assert len(lines) >= 10
+    for name, expr in lines:
+        assert eval(expr, {"__builtins__": {}}, names) == abi.SIGNATURES[name], name
